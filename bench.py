@@ -1,0 +1,294 @@
+"""Measured throughput of the kernel set on one MI355X, next to the CPU path.
+
+    python bench.py [--steps K] [--warmup W] [--all] [--report FILE]
+
+Prints ONE JSON line.  The headline (``value``) is causal attention at
+8 heads x 2048 x d128 bf16 in TFLOP/s, counting the exact causal FLOPs
+4*H*d*S(S+1)/2; the fused softmax / RMSNorm / SwiGLU at 4096 x 2048 bf16 are
+reported in the same line as HBM GB/s and fraction of peak.  ``--all`` adds
+the 1024^3 GEMM, the long-context attention configs and the decoder block.
+
+Timing: every kernel is launched from a captured HIP graph (so host launch
+overhead does not leave the GPU idle between launches), replayed K times
+between two HIP events recorded on the stream the kernels run on; the result
+is the average duration per launch.  Each graph cycles through enough
+distinct input/output buffers (> 256 MB) that no launch finds its data in the
+MI355X's 256 MB last-level cache: the row kernels are measured against HBM.
+
+CPU baseline: the oracle's NumPy restatement of the reference's flash
+algorithm (the "NKI-algorithm CPU path") timed on this host, plus PyTorch CPU
+SDPA, on the same seeded inputs.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "nki-kernel-lab_amd"))
+sys.path.insert(0, ROOT)
+
+METRIC = "causal attn TFLOPS (8h×2048×d128 bf16) + row-kernel HBM GB/s, % of peak"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+LLC_BYTES = 256 << 20       # MI355X Infinity Cache
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def time_launches(launches, reps: int, warmup: int) -> float:
+    """Seconds per launch: capture `launches` (zero-arg callables, one kernel
+    each) into a HIP graph, replay it `warmup` times, then `reps` times between
+    two events on the current stream."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for f in launches:
+            f()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for f in launches:
+            f()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1e-3 / (reps * len(launches))
+
+
+def n_sets(bytes_per_set: int) -> int:
+    """Distinct buffer sets needed so a cyclic sweep overflows the LLC twice over."""
+    return max(2, math.ceil(2 * LLC_BYTES / bytes_per_set))
+
+
+def roofline(bound: str, achieved: float, unit: str, traffic=None) -> dict:
+    peak = PEAK_BF16_TFLOPS if bound == "mfma" else PEAK_HBM_GBS
+    return {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic}
+
+
+# ------------------------------------------------------------ workloads --
+
+def bench_attention(H, S, d, reps, warmup, seed=0, sets=None):
+    import torch
+
+    from nkilab import ops, workloads
+
+    import oracle as O  # noqa: F401  (flop count only)
+
+    q, k, v = (t.cuda() for t in workloads.attention_inputs(H, S, d, seed=seed))
+    per_set = 4 * H * S * d * 2
+    sets = sets or min(n_sets(per_set), 16)
+    bufs = [(q, k, v, torch.empty_like(q))] + [
+        (q.clone(), k.clone(), v.clone(), torch.empty_like(q)) for _ in range(sets - 1)]
+    launches = [lambda b=b: ops.attention_into(*b) for b in bufs]
+    sec = time_launches(launches, reps, warmup)
+    flops = O.causal_flops(H, S, d)
+    return {"H": H, "S": S, "d": d, "us": sec * 1e6, "tflops": flops / sec / 1e12, "flops": flops,
+            "bytes": per_set, "buffer_sets": sets}, bufs[0]
+
+
+def bench_rows(R, D, reps, warmup, seed=0):
+    import torch
+
+    from nkilab import ops, workloads
+
+    x, w, gate, up = (t.cuda() for t in workloads.rows_inputs(R, D, seed=seed))
+    out = {}
+    eb = 2
+    specs = {
+        "softmax": (2 * R * D * eb, lambda xs, ys: ops.softmax_into(xs, ys)),
+        "rmsnorm": (2 * R * D * eb + D * eb, lambda xs, ys: ops.rmsnorm_into(xs, w, ys, 1e-6)),
+    }
+    for name, (nbytes, fn) in specs.items():
+        sets = n_sets(nbytes)
+        bufs = [(x.clone(), torch.empty_like(x)) for _ in range(sets)]
+        sec = time_launches([lambda b=b, fn=fn: fn(*b) for b in bufs], reps, warmup)
+        out[name] = {"us": sec * 1e6, "GB/s": nbytes / sec / 1e9, "bytes": nbytes, "buffer_sets": sets}
+        del bufs
+    nbytes = 3 * R * D * eb
+    sets = n_sets(nbytes)
+    bufs = [(gate.clone(), up.clone(), torch.empty_like(gate)) for _ in range(sets)]
+    sec = time_launches([lambda b=b: ops.swiglu_into(*b) for b in bufs], reps, warmup)
+    out["swiglu"] = {"us": sec * 1e6, "GB/s": nbytes / sec / 1e9, "bytes": nbytes, "buffer_sets": sets}
+    del bufs
+    for r in out.values():
+        r["frac"] = r["GB/s"] / PEAK_HBM_GBS
+    return out
+
+
+def bench_matmul(reps, warmup):
+    import torch
+
+    from nkilab import ops, workloads
+
+    a, b = (t.cuda() for t in workloads.matmul_inputs())
+    sets = n_sets(3 * 1024 * 1024 * 2)
+    bufs = [(a.clone(), b.clone(), torch.empty_like(a)) for _ in range(min(sets, 64))]
+    sec = time_launches([lambda t=t: ops.gemm_into(*t) for t in bufs], reps, warmup)
+    flops = 2 * 1024 ** 3
+    return {"M": 1024, "N": 1024, "K": 1024, "us": sec * 1e6, "tflops": flops / sec / 1e12,
+            "frac": flops / sec / 1e12 / PEAK_BF16_TFLOPS}
+
+
+def bench_decoder(reps, warmup):
+    import torch
+
+    from nkilab import workloads
+    from nkilab.model import nki_forward
+
+    block, x = workloads.decoder_inputs()
+    block = block.cuda()
+    xg = x.cuda()
+    nki_forward(block, xg, compute_dtype="bfloat16")  # fills the weight cache
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        nki_forward(block, xg, compute_dtype="bfloat16")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        nki_forward(block, xg, compute_dtype="bfloat16")
+    torch.cuda.synchronize()
+    sec = (time.perf_counter() - t0) / reps
+    flops = 227_641_655_296
+    return {"us": sec * 1e6, "tflops": flops / sec / 1e12, "frac": flops / sec / 1e12 / PEAK_BF16_TFLOPS,
+            "note": "eager host loop, 9 launches per block, wall clock"}
+
+
+# ---------------------------------------------------------- CPU baseline --
+
+def cpu_baseline(q, k, v, gpu_out):
+    """The oracle's flash attention (NumPy) and PyTorch CPU SDPA on this host."""
+    import numpy as np
+    import torch
+
+    import oracle as O
+
+    H, S, d = q.shape
+    qn, kn, vn = (t.float().cpu().numpy() for t in (q, k, v))
+    flops = O.causal_flops(H, S, d)
+    try:
+        from threadpoolctl import threadpool_info
+        blas_threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
+    except Exception:  # pragma: no cover
+        blas_threads = os.cpu_count() or 1
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        ref = O.ops_attention(qn, kn, vn, "flash_pipelined", O.BF16)
+        reps += 1
+        if time.perf_counter() - t0 > 10.0 or reps >= 8:
+            break
+    sec = (time.perf_counter() - t0) / reps
+    parity = O.rel_err(gpu_out.float().cpu().numpy(), ref)
+    ncores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(ncores)
+    tq, tk, tv = (t.float().cpu() for t in (q, k, v))
+    torch.nn.functional.scaled_dot_product_attention(tq, tk, tv, is_causal=True)
+    t0 = time.perf_counter()
+    torch_reps = 3
+    for _ in range(torch_reps):
+        sdpa = torch.nn.functional.scaled_dot_product_attention(tq, tk, tv, is_causal=True)
+    tsec = (time.perf_counter() - t0) / torch_reps
+    sdpa_err = O.rel_err(gpu_out.float().cpu().numpy(), sdpa.numpy())
+    try:
+        model = next(ln.split(":", 1)[1].strip() for ln in open("/proc/cpuinfo") if ln.startswith("model name"))
+    except Exception:  # pragma: no cover
+        model = "unknown"
+    base = {"value": round(flops / sec / 1e12, 5), "unit": "TFLOP/s", "cores": blas_threads, "kind": "port",
+            "sample": f"full workload {H}x{S}x{d} bf16 values, oracle flash_pipelined (NumPy fp32, 128x128 tiles), "
+                      f"mean of {reps} runs, {sec:.2f} s each",
+            "cpu": model,
+            "torch_cpu_sdpa_fp32": {"value": round(flops / tsec / 1e12, 5), "unit": "TFLOP/s", "cores": ncores,
+                                    "sec": round(tsec, 4)}}
+    return base, {"attention_rel_err_vs_oracle": parity, "attention_rel_err_vs_fp32_sdpa": sdpa_err}
+
+
+# ------------------------------------------------------------------ main --
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--all", action="store_true", help="also the GEMM, long-context and decoder configs")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--report", default=None, help="write the full result dict as JSON here")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(f"bench.py measures one GPU: the kernel set has no multi-GPU path (asked for {args.gpus} GPUs).",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from nkilab import _lib
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 1
+    _lib.lib()
+    props = torch.cuda.get_device_properties(0)
+    log(f"device: {props.name} CUs={props.multi_processor_count} lib={_lib.LIB_PATH}")
+
+    A = dict(H=8, S=2048, d=128)
+    log(f"attention {A} ...")
+    att, bufs = bench_attention(A["H"], A["S"], A["d"], args.steps, args.warmup)
+    log(f"  {att['us']:.2f} us  {att['tflops']:.1f} TFLOP/s")
+    log("row kernels 4096x2048 bf16 ...")
+    rows = bench_rows(4096, 2048, args.steps, args.warmup)
+    for k, r in rows.items():
+        log(f"  {k:8s} {r['us']:.2f} us  {r['GB/s']:.0f} GB/s  {100 * r['frac']:.1f}% of HBM peak")
+
+    result = {
+        "metric": METRIC, "value": round(att["tflops"], 3), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(att["us"] / 1e3, 6),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: N(0,1) bf16 from numpy default_rng(0), no published GPU baseline",
+        "config": {"workload": "causal attention 8 heads x S=2048 x d=128 bf16 (flash, one launch per step)",
+                   "H": 8, "S": 2048, "d": 128,
+                   "flops_per_step": att["flops"], "flop_count": "exact causal pairs 4*H*d*S(S+1)/2",
+                   "device": props.name, "cus": props.multi_processor_count},
+        "roofline": roofline("mfma", att["tflops"], "TFLOP/s"),
+        "row_kernels": {k: {"us": round(r["us"], 3), "GB/s": round(r["GB/s"], 1), "frac": round(r["frac"], 4),
+                            "bytes": r["bytes"], "roofline": roofline("hbm", r["GB/s"], "GB/s")}
+                        for k, r in rows.items()},
+    }
+    if args.all:
+        log("matmul 1024^3 bf16 ...")
+        result["matmul"] = bench_matmul(args.steps, args.warmup)
+        for H, S in ((1, 4096), (32, 16384)):
+            log(f"attention {H}x{S}x128 ...")
+            r, _ = bench_attention(H, S, 128, max(3, args.steps // 10 if S > 4096 else args.steps), args.warmup,
+                                   sets=2 if S > 4096 else None)
+            result[f"attention_{H}x{S}"] = {k: r[k] for k in ("us", "tflops")} | {
+                "frac": r["tflops"] / PEAK_BF16_TFLOPS}
+        log("decoder block ...")
+        result["decoder_block"] = bench_decoder(max(3, args.steps // 10), 2)
+    if not args.no_cpu:
+        log("CPU baseline ...")
+        q, k, v, o = bufs
+        result["cpu_baseline"], result["parity"] = cpu_baseline(q, k, v, o)
+    if args.report:
+        with open(args.report, "w") as f:
+            json.dump(result, f, indent=1)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,155 @@
+/*
+ * nkilab_hip.h -- C ABI of libnkilab_hip.so, the gfx950 (MI355X) kernel set
+ * behind nkilab.ops / nkilab.model.
+ *
+ * Every entry point replaces one `nki.simulate(kernel)(...)` call of the
+ * reference host layer (nkilab/ops.py) and is bound from Python with ctypes
+ * (nkilab/_lib.py).  Conventions shared by all entry points:
+ *
+ *   - Pointers are device pointers allocated by the caller.  The library never
+ *     allocates or frees memory; kernels that need scratch space (the unfused
+ *     softmax, the naive attention) take a caller-provided workspace whose
+ *     size is reported by the matching *_workspace_bytes() function.
+ *   - Strides (ld*, *_sh, *_ss, batch strides) are in ELEMENTS, not bytes.
+ *   - dtype codes: NKL_F32 = 0 (float32), NKL_BF16 = 1 (bfloat16).
+ *   - `stream` is a hipStream_t passed as void* (0 = the null stream).  Every
+ *     call only enqueues work and returns; it is asynchronous with respect to
+ *     the host and re-entrant (no global state besides the per-thread error
+ *     string).
+ *   - Return value: NKL_OK (0) on success, a negative NKL_E* code otherwise;
+ *     nkl_last_error_string() describes the last failure on this thread.
+ */
+#ifndef NKILAB_HIP_H
+#define NKILAB_HIP_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NKL_ABI_VERSION 1
+
+enum { NKL_F32 = 0, NKL_BF16 = 1 };
+
+enum {
+  NKL_OK = 0,
+  NKL_EINVAL = -1,      /* bad shape / stride / argument */
+  NKL_EDTYPE = -2,      /* unsupported dtype combination */
+  NKL_ELAUNCH = -3,     /* the HIP launch failed */
+  NKL_EWORKSPACE = -4,  /* workspace missing or too small */
+  NKL_ELIMIT = -5       /* an on-chip accumulator budget is exceeded */
+};
+
+/* GEMM variants: the reference's two matmul kernels. */
+enum { NKL_GEMM_BLOCKED = 0, NKL_GEMM_NAIVE = 1 };
+
+/* Version of this ABI (NKL_ABI_VERSION). */
+int nkl_abi_version(void);
+
+/* Human-readable description of the last error returned on this thread. */
+const char* nkl_last_error_string(void);
+
+/*
+ * C[b] = A[b] . op(B[b]) (+ R[b]),  b in [0, batch)
+ *
+ * Replaces nkilab/kernels/matmul.py:46 (matmul_blocked, variant
+ * NKL_GEMM_BLOCKED) and nkilab/kernels/matmul.py:24 (matmul_naive, variant
+ * NKL_GEMM_NAIVE), called from nkilab/ops.py:48 and :51.
+ *   A: [M, K] row-major (lda >= K).
+ *   B: b_trans == 0 -> [K, N] row-major (ldb >= N), the reference's `rhs`;
+ *      b_trans == 1 -> [N, K] row-major (ldb >= K), e.g. nn.Linear.weight.
+ *   C: [M, N] row-major (ldc >= N), dtype_out.
+ *   R: optional residual added in the fp32 epilogue ([M, N], ldr, dtype_out);
+ *      NULL for none.
+ * Products accumulate in fp32; C is rounded once (round-to-nearest-even) to
+ * dtype_out.  dtype_in in {F32, BF16}; dtype_out in {F32, dtype_in}.
+ */
+int nkl_gemm(const void* A, const void* B, void* C, const void* R,
+             int M, int N, int K, long lda, long ldb, long ldc, long ldr,
+             int b_trans, int batch, long strideA, long strideB, long strideC,
+             long strideR, int dtype_in, int dtype_out, int variant,
+             void* stream);
+
+/*
+ * The reference's PSUM block check (nkilab/kernels/matmul.py:58): returns
+ * NKL_OK when a BM x BN block of fp32 accumulator tiles fits the 8-tile
+ * budget, NKL_ELIMIT (with a message naming PSUM) otherwise.  Used by the
+ * kernel-level mirror nkilab.kernels.matmul.matmul_blocked.
+ */
+int nkl_check_blocks(int BM, int BN);
+
+/*
+ * y = softmax(x) over the last dimension, fused single pass.
+ * Replaces nkilab/kernels/norm.py:65 (softmax_fused), nkilab/ops.py:57.
+ * x: [rows, cols] (ldx), y: [rows, cols] (ldy), same dtype.  Row max and sum
+ * in fp32, exp(x - max) * (1 / sum) rounded once to dtype.
+ */
+int nkl_softmax(const void* x, void* y, int rows, int cols, long ldx,
+                long ldy, int dtype, void* stream);
+
+/*
+ * Three-pass softmax through HBM (max -> exp & sum -> divide).
+ * Replaces nkilab/kernels/norm.py:22 (softmax_unfused), nkilab/ops.py:56-57
+ * with fused=False.  The fp32 intermediates live in `workspace`
+ * (nkl_softmax_unfused_workspace_bytes(rows, cols) bytes, 256-byte aligned).
+ */
+size_t nkl_softmax_unfused_workspace_bytes(int rows, int cols);
+int nkl_softmax_unfused(const void* x, void* y, void* workspace,
+                        size_t workspace_bytes, int rows, int cols, long ldx,
+                        long ldy, int dtype, void* stream);
+
+/*
+ * y = x * rsqrt(mean(x^2) + eps) * w.
+ * Replaces nkilab/kernels/norm.py:92 (rmsnorm_fused), nkilab/ops.py:61.
+ * x: [rows, cols] (ldx, dtype_in); w: [cols] (dtype_in); y: (ldy, dtype_out).
+ * dtype_out in {dtype_in, BF16}: an fp32 residual stream can be normalised
+ * straight into a bf16 GEMM operand.
+ */
+int nkl_rmsnorm(const void* x, const void* w, void* y, int rows, int cols,
+                long ldx, long ldy, float eps, int dtype_in, int dtype_out,
+                void* stream);
+
+/*
+ * y = silu(g) * u, element-wise over n contiguous elements.
+ * Replaces nkilab/kernels/norm.py:121 (swiglu_fused), nkilab/ops.py:65.
+ */
+int nkl_swiglu(const void* g, const void* u, void* y, long n, int dtype,
+               void* stream);
+
+/*
+ * Causal attention O = softmax(Q K^T * scale + causal mask) V, flash style:
+ * online softmax over key tiles, key tiles wholly above the diagonal are
+ * skipped, the diagonal tiles are masked (key > query).
+ * Replaces nkilab/kernels/attention.py:280 (flash_attention_pipelined, the
+ * default of nkilab/ops.py:77) and its numerically identical siblings
+ * attention.py:155, :179, :249; called from nkilab/ops.py:90.
+ * q, k, v, o: [H, S, d] with element strides (*_sh between heads, *_ss between
+ * positions) and unit stride along d; any S >= 1, 1 <= d <= 128.
+ * bf16: P is rounded to bf16 before P.V, statistics and O accumulate in fp32,
+ * O is rounded once.  f32: everything in fp32.
+ */
+int nkl_flash_attn_causal(const void* q, const void* k, const void* v,
+                          void* o, int H, int S, int d, long q_sh, long q_ss,
+                          long k_sh, long k_ss, long v_sh, long v_ss,
+                          long o_sh, long o_ss, float scale, int dtype,
+                          void* stream);
+
+/*
+ * Unfused causal attention: scores (fp32, [H, S, S]) and probabilities
+ * ([H, S, S], dtype) are materialised in `workspace`, then O = P V.
+ * Replaces nkilab/kernels/attention.py:35 (attention_naive), selected by
+ * variant "naive" at nkilab/ops.py:68-74.
+ */
+size_t nkl_attention_naive_workspace_bytes(int H, int S, int dtype);
+int nkl_attention_naive(const void* q, const void* k, const void* v, void* o,
+                        void* workspace, size_t workspace_bytes, int H, int S,
+                        int d, long q_sh, long q_ss, long k_sh, long k_ss,
+                        long v_sh, long v_ss, long o_sh, long o_ss,
+                        float scale, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NKILAB_HIP_H */

@@ -1,0 +1,417 @@
+// Causal attention on gfx950.
+//
+// flash_fwd_kernel -- the hot path.  One 256-thread workgroup owns BM = 64
+// consecutive queries of one head; each of its four wavefronts owns 16 of
+// them.  Key/value tiles of BN keys stream through double-buffered LDS and
+// the running softmax state (max, sum, output) stays in registers, so
+// scores never leave the chip.  Key tiles entirely above the diagonal are
+// never visited; the tiles that straddle it are masked element-wise.
+//
+// Everything is computed transposed so that each lane always works on a
+// single query:
+//     S^T = K . Q^T      (A = K rows from LDS, B = Q^T fragments in VGPRs)
+//     O^T = V^T . P^T    (A = V^T from LDS,    B = P^T straight from S^T)
+// With 16x16 MFMAs, lane l holds query l % 16 of its wavefront in both the
+// S^T and O^T accumulators, so the running max / sum / correction factor are
+// per-lane scalars, and the probabilities produced by the exp are already in
+// the B-operand layout of the P.V MFMA (no shuffle, no LDS round trip).
+// For bf16 the V tile is written to LDS transposed and key-permuted so that
+// the V^T operand is one 16-byte read per MFMA.
+//
+// attention_naive -- the reference's unfused variant: scores and
+// probabilities are materialised in a caller-provided workspace, using the
+// GEMM kernels for Q.K^T and P.V and a masked row softmax in between.
+#include <math.h>
+
+#include "common.h"
+
+namespace nkl {
+
+struct AttnArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  int H, S, d;
+  long q_sh, q_ss, k_sh, k_ss, v_sh, v_ss, o_sh, o_ss;
+  float c;  // softmax scale * log2(e): p = exp2(s * c - m)
+};
+
+template <typename T>
+struct FlashCfg;
+template <>
+struct FlashCfg<bf16> { static constexpr int BN = 64; };
+template <>
+struct FlashCfg<float> { static constexpr int BN = 32; };
+
+// bf16 V^T layout: within a tile of 64 keys, key kk = 16 * kb + 4 * g + i
+// (kb < 4, g < 4, i < 4) is stored at column 32 * (kb / 2) + 8 * g +
+// 4 * (kb % 2) + i, so that lane group g's eight keys of MFMA t = kb / 2 are
+// contiguous -- the same order in which the lane holds their probabilities.
+__device__ __forceinline__ int vt_col(int kk) {
+  const int kb = kk >> 4, g = (kk >> 2) & 3, i = kk & 3;
+  return 32 * (kb >> 1) + 8 * g + 4 * (kb & 1) + i;
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void flash_fwd_kernel(AttnArgs p) {
+  using MF = Mfma16<T>;
+  constexpr bool BF = sizeof(T) == 2;
+  constexpr int BM = 64;
+  constexpr int BN = FlashCfg<T>::BN;
+  constexpr int E = VecE<T>::value;      // elements per 16-byte chunk
+  constexpr int CPR = D / E;             // 16-byte chunks per K/V row
+  constexpr int LDK = D + E;             // K (and f32 V) LDS row stride, padded
+  constexpr int LDV = BN + 8;            // bf16 V^T LDS row stride, padded
+  constexpr int K_CH = BN * CPR / 256;   // K chunks per thread
+  constexpr int NKB = BN / 16;           // 16-key sub-blocks per tile
+  constexpr int ND = D / 16;             // 16-wide d blocks of O^T
+  constexpr int NQF = D / MF::MK;        // Q fragments per lane
+  static_assert(K_CH >= 1 && (BN * CPR) % 256 == 0, "tile does not split over 256 threads");
+
+  constexpr int V_ELEMS = BF ? D * LDV : BN * LDK;
+  __shared__ T Ks[2][BN * LDK];
+  __shared__ T Vs[2][V_ELEMS];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = lane >> 4, r = lane & 15;
+  const int S = p.S, dlim = p.d;
+
+  // Heavy-first: the first workgroups dispatched take the query blocks with
+  // the most key tiles; consecutive ids walk the heads, so with 8 heads head
+  // h always lands on XCD h and its K/V stay in one L2.
+  const int nqb = (S + BM - 1) / BM;
+  const int h = blockIdx.x % p.H;
+  const int qb = nqb - 1 - blockIdx.x / p.H;
+  const int q0 = qb * BM;
+  const int qw = q0 + 16 * w;   // first query of this wavefront
+  const int myq = qw + r;       // this lane's query
+
+  const T* Q = static_cast<const T*>(p.q) + (long)h * p.q_sh;
+  const T* K = static_cast<const T*>(p.k) + (long)h * p.k_sh;
+  const T* V = static_cast<const T*>(p.v) + (long)h * p.v_sh;
+  T* O = static_cast<T*>(p.o) + (long)h * p.o_sh;
+
+  // Q^T fragments: lane (r, g) holds Q[myq][MK * f + KPER * g + j].
+  typename MF::frag qf[NQF];
+#pragma unroll
+  for (int f = 0; f < NQF; ++f) {
+    const int dd = f * MF::MK + g * MF::KPER;
+    if constexpr (BF) {
+      if (myq < S && dd < dlim)
+        qf[f] = load_frag(Q + (long)myq * p.q_ss + dd);
+      else
+#pragma unroll
+        for (int j = 0; j < 8; ++j) qf[f][j] = (bf16)0.f;
+    } else {
+      qf[f] = (myq < S && dd < dlim) ? Q[(long)myq * p.q_ss + dd] : 0.f;
+    }
+  }
+
+  // ---- K/V staging: global -> registers -> LDS.
+  uint4 rk[K_CH];
+  // bf16 V: a thread moves 4 consecutive keys x 8 d values.
+  constexpr int V_GRP = BF ? (BN / 4) * (D / 8) : 0;
+  constexpr int V_IT = BF ? (V_GRP + 255) / 256 : K_CH;
+  uint4 rv[BF ? V_IT * 4 : K_CH];
+  const uint4 zero = make_uint4(0, 0, 0, 0);
+
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < K_CH; ++i) {
+      const int c = tid + 256 * i, row = c / CPR, cc = (c % CPR) * E;
+      const int key = k0 + row;
+      rk[i] = (key < S && cc < dlim) ? *reinterpret_cast<const uint4*>(K + (long)key * p.k_ss + cc) : zero;
+      if constexpr (!BF)
+        rv[i] = (key < S && cc < dlim) ? *reinterpret_cast<const uint4*>(V + (long)key * p.v_ss + cc) : zero;
+    }
+    if constexpr (BF) {
+#pragma unroll
+      for (int it = 0; it < V_IT; ++it) {
+        const int grp = tid + 256 * it;
+        const int kg = grp % (BN / 4), dc = (grp / (BN / 4)) * 8;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int key = k0 + 4 * kg + rr;
+          rv[it * 4 + rr] = (grp < V_GRP && key < S && dc < dlim)
+                                ? *reinterpret_cast<const uint4*>(V + (long)key * p.v_ss + dc)
+                                : zero;
+        }
+      }
+    }
+  };
+
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < K_CH; ++i) {
+      const int c = tid + 256 * i, row = c / CPR, cc = (c % CPR) * E;
+      *reinterpret_cast<uint4*>(&Ks[buf][row * LDK + cc]) = rk[i];
+      if constexpr (!BF) *reinterpret_cast<uint4*>(&Vs[buf][row * LDK + cc]) = rv[i];
+    }
+    if constexpr (BF) {
+#pragma unroll
+      for (int it = 0; it < V_IT; ++it) {
+        const int grp = tid + 256 * it;
+        if (grp < V_GRP) {
+          const int kg = grp % (BN / 4), dc = (grp / (BN / 4)) * 8;
+          const int col = vt_col(4 * kg);
+          const uint32_t* a0 = reinterpret_cast<const uint32_t*>(&rv[it * 4 + 0]);
+          const uint32_t* a1 = reinterpret_cast<const uint32_t*>(&rv[it * 4 + 1]);
+          const uint32_t* a2 = reinterpret_cast<const uint32_t*>(&rv[it * 4 + 2]);
+          const uint32_t* a3 = reinterpret_cast<const uint32_t*>(&rv[it * 4 + 3]);
+#pragma unroll
+          for (int jj = 0; jj < 8; ++jj) {
+            const int wd = jj >> 1;
+            uint2 t;
+            if (jj & 1) {
+              t.x = (a0[wd] >> 16) | (a1[wd] & 0xffff0000u);
+              t.y = (a2[wd] >> 16) | (a3[wd] & 0xffff0000u);
+            } else {
+              t.x = (a0[wd] & 0xffffu) | (a1[wd] << 16);
+              t.y = (a2[wd] & 0xffffu) | (a3[wd] << 16);
+            }
+            *reinterpret_cast<uint2*>(&Vs[buf][(dc + jj) * LDV + col]) = t;
+          }
+        }
+      }
+    }
+  };
+
+  // ---- running state for query myq
+  float m_run = -INFINITY;  // running max of s * c
+  float l_run = 0.f;        // this lane's share of the running sum
+  floatx4 oacc[ND];
+#pragma unroll
+  for (int db = 0; db < ND; ++db) oacc[db] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  const int q_last = min(q0 + BM, S) - 1;
+  const int nkt = q_last / BN + 1;  // key tiles 0 .. nkt-1 (the rest are above the diagonal)
+  const int wq_last = qw + 15;
+
+  gload(0);
+  lstore(0);
+  __syncthreads();
+
+  for (int jt = 0; jt < nkt; ++jt) {
+    const int buf = jt & 1;
+    const int k0 = jt * BN;
+    if (jt + 1 < nkt) gload(k0 + BN);
+
+    // S^T = K . Q^T for this wavefront's 16 queries.
+    floatx4 sacc[NKB];
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      sacc[kb] = floatx4{0.f, 0.f, 0.f, 0.f};
+      if (k0 + 16 * kb <= wq_last) {
+#pragma unroll
+        for (int f = 0; f < NQF; ++f) {
+          const typename MF::frag a = load_frag(&Ks[buf][(16 * kb + r) * LDK + f * MF::MK + g * MF::KPER]);
+          sacc[kb] = MF::mma(a, qf[f], sacc[kb]);
+        }
+      }
+    }
+
+    // Online softmax.  Element i of sacc[kb] is key k0 + 16 kb + 4 g + i.
+    const bool diag = k0 + BN - 1 > qw;
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float s = sacc[kb][i] * p.c;
+        if (diag && k0 + 16 * kb + 4 * g + i > myq) s = -INFINITY;
+        sacc[kb][i] = s;
+        mloc = fmaxf(mloc, s);
+      }
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 16, kWave));
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave));
+    const float m_new = fmaxf(m_run, mloc);
+    const float corr = fast_exp2(m_run - m_new);
+    m_run = m_new;
+    float rsum = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float e = fast_exp2(sacc[kb][i] - m_new);
+        sacc[kb][i] = e;
+        rsum += e;
+      }
+    l_run = fmaf(l_run, corr, rsum);
+#pragma unroll
+    for (int db = 0; db < ND; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) oacc[db][i] *= corr;
+
+    // O^T += V^T . P^T
+    if constexpr (BF) {
+#pragma unroll
+      for (int t = 0; t < BN / 32; ++t) {
+        if (k0 + 32 * t > wq_last) continue;
+        bf16x8 pf;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pf[i] = (bf16)sacc[2 * t][i];
+          pf[4 + i] = (bf16)sacc[2 * t + 1][i];
+        }
+#pragma unroll
+        for (int db = 0; db < ND; ++db) {
+          const bf16x8 a = load_frag(&Vs[buf][(16 * db + r) * LDV + 32 * t + 8 * g]);
+          oacc[db] = MF::mma(a, pf, oacc[db]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        if (k0 + 16 * kb > wq_last) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int db = 0; db < ND; ++db) {
+            const float a = Vs[buf][(16 * kb + 4 * g + i) * LDK + 16 * db + r];
+            oacc[db] = MF::mma(a, sacc[kb][i], oacc[db]);
+          }
+      }
+    }
+
+    if (jt + 1 < nkt) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Finish: l = sum over the four lane groups; O = O^T / l rounded once.
+  float l = l_run + __shfl_xor(l_run, 16, kWave);
+  l += __shfl_xor(l, 32, kWave);
+  const float linv = 1.0f / l;
+  if (myq < S) {
+    T* orow = O + (long)myq * p.o_ss;
+#pragma unroll
+    for (int db = 0; db < ND; ++db) {
+      const int dd = 16 * db + 4 * g;
+      if (dd < dlim) {
+        float ov[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ov[i] = oacc[db][i] * linv;
+        store_vec<4>(orow + dd, ov);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------ naive (unfused) path --
+// nkilab/kernels/attention.py:35-89, pass 2: scores (already Q.K^T) are
+// scaled and causally masked, then a row softmax writes P in the input dtype.
+template <typename T>
+__global__ __launch_bounds__(256) void masked_softmax_kernel(float* __restrict__ sc, T* __restrict__ pr, int H,
+                                                             int S, float scale) {
+  const int lane = threadIdx.x & 63;
+  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);  // (h, q) flattened
+  if (row >= (long)H * S) return;
+  const int q = (int)(row % S);
+  float* srow = sc + row * S;
+  T* prow = pr + row * S;
+  float mx = -INFINITY;
+  for (int c = lane; c < S; c += kWave) {
+    const float s = c > q ? -INFINITY : srow[c] * scale;
+    srow[c] = s;
+    mx = fmaxf(mx, s);
+  }
+  mx = wave_max(mx);
+  float sum = 0.f;
+  for (int c = lane; c < S; c += kWave) sum += fast_exp2((srow[c] - mx) * kLog2e);
+  sum = wave_sum(sum);
+  const float rinv = 1.0f / sum;
+  for (int c = lane; c < S; c += kWave) prow[c] = from_f32<T>(fast_exp2((srow[c] - mx) * kLog2e) * rinv);
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+template <typename T, int D>
+static void flash_launch(const AttnArgs& a, hipStream_t st) {
+  const int nqb = (a.S + 63) / 64;
+  flash_fwd_kernel<T, D><<<dim3((unsigned)(nqb * a.H)), dim3(256), 0, st>>>(a);
+}
+
+template <typename T>
+static int flash_dispatch(const AttnArgs& a, hipStream_t st) {
+  if (a.d <= 32)
+    flash_launch<T, 32>(a, st);
+  else if (a.d <= 64)
+    flash_launch<T, 64>(a, st);
+  else
+    flash_launch<T, 128>(a, st);
+  return check_launch("nkl_flash_attn_causal");
+}
+
+}  // namespace nkl
+
+using namespace nkl;
+
+static int check_attn(const char* fn, const void* q, const void* k, const void* v, const void* o, int H, int S,
+                      int d, int dtype, const long* strides) {
+  if (H < 0 || S < 0) return set_error(NKL_EINVAL, "%s: negative shape H=%d S=%d", fn, H, S);
+  if (d < 1 || d > 128) return set_error(NKL_EINVAL, "%s: head dim d=%d outside [1, 128]", fn, d);
+  if (dtype != NKL_F32 && dtype != NKL_BF16) return set_error(NKL_EDTYPE, "%s: unsupported dtype %d", fn, dtype);
+  const int E = dtype == NKL_F32 ? 4 : 8;
+  if (d % E != 0)
+    return set_error(NKL_EINVAL, "%s: d=%d must be a multiple of %d (pad the head dim on the host)", fn, d, E);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+    return set_error(NKL_EINVAL, "%s: q/k/v/o must be 16-byte aligned", fn);
+  for (int i = 0; i < 8; ++i)
+    if (strides[i] % E != 0)
+      return set_error(NKL_EINVAL, "%s: stride %ld is not a multiple of %d elements", fn, strides[i], E);
+  return NKL_OK;
+}
+
+extern "C" int nkl_flash_attn_causal(const void* q, const void* k, const void* v, void* o, int H, int S, int d,
+                                     long q_sh, long q_ss, long k_sh, long k_ss, long v_sh, long v_ss, long o_sh,
+                                     long o_ss, float scale, int dtype, void* stream) {
+  const long strides[8] = {q_sh, q_ss, k_sh, k_ss, v_sh, v_ss, o_sh, o_ss};
+  int rc = check_attn("nkl_flash_attn_causal", q, k, v, o, H, S, d, dtype, strides);
+  if (rc) return rc;
+  if (H == 0 || S == 0) return NKL_OK;
+  AttnArgs a{q, k, v, o, H, S, d, q_sh, q_ss, k_sh, k_ss, v_sh, v_ss, o_sh, o_ss, scale * kLog2e};
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == NKL_BF16) return flash_dispatch<bf16>(a, st);
+  return flash_dispatch<float>(a, st);
+}
+
+extern "C" size_t nkl_attention_naive_workspace_bytes(int H, int S, int dtype) {
+  if (H <= 0 || S <= 0) return 0;
+  const size_t n = (size_t)H * S * S;
+  const size_t sc = (n * 4 + 255) / 256 * 256;
+  return sc + n * (dtype == NKL_F32 ? 4 : 2);
+}
+
+extern "C" int nkl_attention_naive(const void* q, const void* k, const void* v, void* o, void* workspace,
+                                   size_t workspace_bytes, int H, int S, int d, long q_sh, long q_ss, long k_sh,
+                                   long k_ss, long v_sh, long v_ss, long o_sh, long o_ss, float scale, int dtype,
+                                   void* stream) {
+  const long strides[8] = {q_sh, q_ss, k_sh, k_ss, v_sh, v_ss, o_sh, o_ss};
+  int rc = check_attn("nkl_attention_naive", q, k, v, o, H, S, d, dtype, strides);
+  if (rc) return rc;
+  if (H == 0 || S == 0) return NKL_OK;
+  const size_t need = nkl_attention_naive_workspace_bytes(H, S, dtype);
+  if (!workspace || workspace_bytes < need)
+    return set_error(NKL_EWORKSPACE, "nkl_attention_naive: workspace of %zu bytes needed, %zu given", need,
+                     workspace_bytes);
+  const size_t n = (size_t)H * S * S;
+  float* sc = static_cast<float*>(workspace);
+  void* pr = static_cast<char*>(workspace) + (n * 4 + 255) / 256 * 256;
+  hipStream_t st = (hipStream_t)stream;
+  const long SS = (long)S * S;
+  // pass 1: scores[h] = Q[h] . K[h]^T (fp32)
+  rc = nkl_gemm(q, k, sc, nullptr, S, S, d, q_ss, k_ss, S, 0, 1, H, q_sh, k_sh, SS, 0, dtype, NKL_F32,
+                NKL_GEMM_BLOCKED, stream);
+  if (rc) return rc;
+  // pass 2: scale, mask, row softmax -> P
+  const dim3 grid((unsigned)(((long)H * S + 3) / 4)), block(256);
+  if (dtype == NKL_BF16)
+    masked_softmax_kernel<bf16><<<grid, block, 0, st>>>(sc, static_cast<bf16*>(pr), H, S, scale);
+  else
+    masked_softmax_kernel<float><<<grid, block, 0, st>>>(sc, static_cast<float*>(pr), H, S, scale);
+  rc = check_launch("nkl_attention_naive(softmax)");
+  if (rc) return rc;
+  // pass 3: O[h] = P[h] . V[h]
+  return nkl_gemm(pr, v, o, nullptr, S, d, S, S, v_ss, o_ss, 0, 0, H, SS, v_sh, o_sh, 0, dtype, dtype,
+                  NKL_GEMM_BLOCKED, stream);
+}

@@ -1,0 +1,169 @@
+// Shared device helpers for the gfx950 kernels: element types, 16-byte
+// vector loads/stores, bf16 rounding, wavefront reductions and the MFMA
+// operand traits used by the GEMM and attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/nkilab_hip.h"
+
+namespace nkl {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- scalars --
+
+template <typename T>
+__device__ __forceinline__ float to_f32(T v);
+template <>
+__device__ __forceinline__ float to_f32<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ float to_f32<bf16>(bf16 v) { return (float)v; }
+
+// fp32 -> T, round-to-nearest-even (v_cvt_pk_bf16_f32 on gfx950).
+template <typename T>
+__device__ __forceinline__ T from_f32(float v);
+template <>
+__device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ bf16 from_f32<bf16>(float v) { return (bf16)v; }
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  bf16x2 r;
+  r[0] = (bf16)lo;
+  r[1] = (bf16)hi;
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+__device__ __forceinline__ float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ------------------------------------------------------- 16-byte vectors --
+// VecE<T> = number of T elements in one 16-byte load.
+template <typename T>
+struct VecE { static constexpr int value = 16 / sizeof(T); };
+
+// Load one 16-byte vector of T as fp32 values.
+__device__ __forceinline__ void load16(const float* p, float (&v)[4]) {
+  float4 t = *reinterpret_cast<const float4*>(p);
+  v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+}
+__device__ __forceinline__ void load16(const bf16* p, float (&v)[8]) {
+  uint4 t = *reinterpret_cast<const uint4*>(p);
+  v[0] = bf16lo(t.x); v[1] = bf16hi(t.x);
+  v[2] = bf16lo(t.y); v[3] = bf16hi(t.y);
+  v[4] = bf16lo(t.z); v[5] = bf16hi(t.z);
+  v[6] = bf16lo(t.w); v[7] = bf16hi(t.w);
+}
+
+// Store E fp32 values as E elements of T (E * sizeof(T) bytes, aligned).
+template <int E>
+__device__ __forceinline__ void store_vec(float* p, const float (&v)[E]) {
+#pragma unroll
+  for (int i = 0; i < E; i += 4)
+    *reinterpret_cast<float4*>(p + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+}
+template <int E>
+__device__ __forceinline__ void store_vec(bf16* p, const float (&v)[E]) {
+  static_assert(E == 4 || E == 8, "bf16 vector store of 4 or 8 elements");
+  if constexpr (E == 8) {
+    uint4 t;
+    t.x = pack_bf16x2(v[0], v[1]);
+    t.y = pack_bf16x2(v[2], v[3]);
+    t.z = pack_bf16x2(v[4], v[5]);
+    t.w = pack_bf16x2(v[6], v[7]);
+    *reinterpret_cast<uint4*>(p) = t;
+  } else {
+    uint2 t;
+    t.x = pack_bf16x2(v[0], v[1]);
+    t.y = pack_bf16x2(v[2], v[3]);
+    *reinterpret_cast<uint2*>(p) = t;
+  }
+}
+
+// ------------------------------------------------------ wave reductions --
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// ------------------------------------------------------- MFMA operands --
+// A 16x16 (M x N) MFMA with K = 4 * KPER: lane l holds
+//   A[m = l % 16][k = KPER * (l / 16) + j], B[k = KPER * (l / 16) + j][n = l % 16]
+// for j < KPER, and the accumulator C[4 * (l / 16) + i][l % 16], i < 4.
+template <typename T>
+struct Mfma16;
+template <>
+struct Mfma16<bf16> {
+  static constexpr int KPER = 8;
+  static constexpr int MK = 32;
+  typedef bf16x8 frag;
+  static __device__ __forceinline__ floatx4 mma(frag a, frag b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma16<float> {
+  static constexpr int KPER = 1;
+  static constexpr int MK = 4;
+  typedef float frag;
+  static __device__ __forceinline__ floatx4 mma(frag a, frag b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+};
+
+// A 32x32 MFMA with K = 2 * KPER: lane l holds
+//   A[m = l % 32][k = KPER * (l / 32) + j], B[k = KPER * (l / 32) + j][n = l % 32]
+// and the accumulator C[8 * (i / 4) + 4 * (l / 32) + i % 4][l % 32], i < 16.
+template <typename T>
+struct Mfma32;
+template <>
+struct Mfma32<bf16> {
+  static constexpr int KPER = 8;
+  static constexpr int MK = 16;
+  typedef bf16x8 frag;
+  static __device__ __forceinline__ floatx16 mma(frag a, frag b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma32<float> {
+  static constexpr int KPER = 1;
+  static constexpr int MK = 2;
+  typedef float frag;
+  static __device__ __forceinline__ floatx16 mma(frag a, frag b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+  }
+};
+
+// Load KPER consecutive elements as one MFMA operand fragment.
+__device__ __forceinline__ bf16x8 load_frag(const bf16* p) {
+  return *reinterpret_cast<const bf16x8*>(p);
+}
+__device__ __forceinline__ float load_frag(const float* p) { return *p; }
+
+}  // namespace nkl
+
+// ----------------------------------------------------- host-side helpers --
+namespace nkl {
+// Records `msg` as this thread's last error and returns `code`.
+int set_error(int code, const char* fmt, ...);
+// Checks hipGetLastError() after a launch; returns NKL_OK or NKL_ELAUNCH.
+int check_launch(const char* what);
+}  // namespace nkl

@@ -1,0 +1,308 @@
+// GEMM: C = A . op(B) (+ R) on 32x32 MFMA tiles with fp32 accumulation.
+//
+// Blocked kernel (the hot path): a 256-thread workgroup owns a BM x BN tile
+// of C; its four wavefronts are laid out 2 x 2 and each owns a
+// (BM/2) x (BN/2) sub-tile of 32x32 MFMA accumulators.  Per K step of BK
+// elements (64 bytes of each operand row) the workgroup stages an A tile
+// [BM][BK] and a B tile [BN][BK] in LDS, both K-contiguous so that every MFMA
+// operand fragment is one 16-byte LDS read.  B given as [K, N] (the
+// reference's `rhs`) is transposed while it is written to LDS; B given as
+// [N, K] (nn.Linear.weight) is copied as is.  LDS is double-buffered and the
+// next K step's global loads are in flight while the current one computes.
+//
+// Naive kernel (variant "naive", and the fallback for shapes the blocked
+// kernel's 16-byte loads cannot address): each wavefront computes one 32x32
+// tile of C reading its operands straight from global memory at every K step
+// -- no on-chip reuse, like the reference's matmul_naive.
+#include "common.h"
+
+namespace nkl {
+
+struct GemmArgs {
+  const void* A;
+  const void* B;
+  void* C;
+  const void* R;
+  int M, N, K;
+  long lda, ldb, ldc, ldr;
+  long sA, sB, sC, sR;
+};
+
+template <typename T>
+struct GemmBK { static constexpr int value = 64 / sizeof(T); };
+
+// Workgroup tile index -> (tile_m, tile_n).  Consecutive workgroup ids are
+// dispatched round-robin over the 8 XCDs; the remap gives each XCD a
+// contiguous range of tiles, walked in groups of GROUP_M tile-rows so the
+// A and B stripes a group touches stay in that XCD's L2.
+__device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int total = tiles_m * tiles_n;
+  int id = bid;
+  if (total % 8 == 0) id = (bid % 8) * (total / 8) + bid / 8;
+  constexpr int GROUP_M = 8;
+  const int group_size = GROUP_M * tiles_n;
+  const int group = id / group_size;
+  const int first_m = group * GROUP_M;
+  const int gm = min(tiles_m - first_m, GROUP_M);
+  const int in_group = id - group * group_size;
+  tm = first_m + in_group % gm;
+  tn = in_group / gm;
+}
+
+template <typename T, typename TO, int BM, int BN, bool BT>
+__global__ __launch_bounds__(256) void gemm_blocked_kernel(GemmArgs p) {
+  using MF = Mfma32<T>;
+  constexpr int E = VecE<T>::value;           // elements per 16-byte chunk
+  constexpr int BK = GemmBK<T>::value;        // K elements per stage (64 bytes)
+  constexpr int PAD = E;                      // 16 bytes of row padding
+  constexpr int LDK = BK + PAD;               // LDS row stride (elements)
+  constexpr int CPR = BK / E;                 // 16-byte chunks per LDS row (4)
+  constexpr int WM = BM / 2, WN = BN / 2;     // wave sub-tile
+  constexpr int TM = WM / 32, TN = WN / 32;   // 32x32 MFMA tiles per wave
+  constexpr int A_CH = BM * CPR / 256;        // A chunks per thread
+  constexpr int B_CH = BN * CPR / 256;        // B chunks per thread
+  static_assert(A_CH >= 1 && B_CH >= 1, "tile too small for 256 threads");
+
+  __shared__ T As[2][BM * LDK];
+  __shared__ T Bs[2][BN * LDK];
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int wm = wid >> 1, wn = wid & 1;
+  const int tiles_m = (p.M + BM - 1) / BM, tiles_n = (p.N + BN - 1) / BN;
+  int tm, tn;
+  tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int bz = blockIdx.z;
+  const T* A = static_cast<const T*>(p.A) + (long)bz * p.sA;
+  const T* B = static_cast<const T*>(p.B) + (long)bz * p.sB;
+  TO* C = static_cast<TO*>(p.C) + (long)bz * p.sC;
+  const TO* R = p.R ? static_cast<const TO*>(p.R) + (long)bz * p.sR : nullptr;
+
+  uint4 ra[A_CH], rb[B_CH];
+  const uint4 zero = make_uint4(0, 0, 0, 0);
+
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) {
+      const int c = tid + 256 * i, row = c / CPR, kc = (c % CPR) * E;
+      const int gm = m0 + row, gk = k0 + kc;
+      ra[i] = (gm < p.M && gk < p.K) ? *reinterpret_cast<const uint4*>(A + (long)gm * p.lda + gk) : zero;
+    }
+    if constexpr (BT) {
+#pragma unroll
+      for (int i = 0; i < B_CH; ++i) {
+        const int c = tid + 256 * i, row = c / CPR, kc = (c % CPR) * E;
+        const int gn = n0 + row, gk = k0 + kc;
+        rb[i] = (gn < p.N && gk < p.K) ? *reinterpret_cast<const uint4*>(B + (long)gn * p.ldb + gk) : zero;
+      }
+    } else {
+      constexpr int NCH = BN / E;  // 16-byte chunks per B row of the tile
+#pragma unroll
+      for (int i = 0; i < B_CH; ++i) {
+        const int c = tid + 256 * i, kr = c / NCH, nc = (c % NCH) * E;
+        const int gk = k0 + kr, gn = n0 + nc;
+        rb[i] = (gk < p.K && gn < p.N) ? *reinterpret_cast<const uint4*>(B + (long)gk * p.ldb + gn) : zero;
+      }
+    }
+  };
+
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) {
+      const int c = tid + 256 * i, row = c / CPR, kc = (c % CPR) * E;
+      *reinterpret_cast<uint4*>(&As[buf][row * LDK + kc]) = ra[i];
+    }
+    if constexpr (BT) {
+#pragma unroll
+      for (int i = 0; i < B_CH; ++i) {
+        const int c = tid + 256 * i, row = c / CPR, kc = (c % CPR) * E;
+        *reinterpret_cast<uint4*>(&Bs[buf][row * LDK + kc]) = rb[i];
+      }
+    } else {
+      constexpr int NCH = BN / E;
+#pragma unroll
+      for (int i = 0; i < B_CH; ++i) {
+        const int c = tid + 256 * i, kr = c / NCH, nc = (c % NCH) * E;
+        const T* v = reinterpret_cast<const T*>(&rb[i]);
+#pragma unroll
+        for (int e = 0; e < E; ++e) Bs[buf][(nc + e) * LDK + kr] = v[e];
+      }
+    }
+  };
+
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  const int nk = (p.K + BK - 1) / BK;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  const int lr = lane & 31, lg = lane >> 5;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) gload((kt + 1) * BK);
+#pragma unroll
+    for (int ks = 0; ks < BK / MF::MK; ++ks) {
+      const int kk = ks * MF::MK + lg * MF::KPER;
+      typename MF::frag af[TM], bfr[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[i] = load_frag(&As[buf][(wm * WM + i * 32 + lr) * LDK + kk]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bfr[j] = load_frag(&Bs[buf][(wn * WN + j * 32 + lr) * LDK + kk]);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = MF::mma(af[i], bfr[j], acc[i][j]);
+    }
+    if (kt + 1 < nk) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue: accumulator element e of tile (i, j) is C[row][col] with
+  // row = 8 * (e / 4) + 4 * (lane / 32) + e % 4, col = lane % 32.
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = n0 + wn * WN + j * 32 + lr;
+      if (col >= p.N) continue;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = m0 + wm * WM + i * 32 + 8 * (e / 4) + 4 * lg + (e % 4);
+        if (row < p.M) {
+          float vv = acc[i][j][e];
+          if (R) vv += to_f32(R[(long)row * p.ldr + col]);
+          C[(long)row * p.ldc + col] = from_f32<TO>(vv);
+        }
+      }
+    }
+}
+
+// One wavefront per 32x32 tile of C, four per workgroup; operands are read
+// from global memory at every K step with per-element bounds checks.
+template <typename T, typename TO, bool BT>
+__global__ __launch_bounds__(256) void gemm_naive_kernel(GemmArgs p) {
+  using MF = Mfma32<T>;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int tiles_n = (p.N + 31) / 32;
+  const int tile = blockIdx.x * 4 + wid;
+  const int tm = tile / tiles_n, tn = tile % tiles_n;
+  if (tm * 32 >= p.M) return;
+  const int bz = blockIdx.z;
+  const T* A = static_cast<const T*>(p.A) + (long)bz * p.sA;
+  const T* B = static_cast<const T*>(p.B) + (long)bz * p.sB;
+  TO* C = static_cast<TO*>(p.C) + (long)bz * p.sC;
+  const TO* R = p.R ? static_cast<const TO*>(p.R) + (long)bz * p.sR : nullptr;
+  const int lr = lane & 31, lg = lane >> 5;
+  const int arow = tm * 32 + lr, bcol = tn * 32 + lr;
+  floatx16 acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+  for (int k0 = 0; k0 < p.K; k0 += MF::MK) {
+    T av[MF::KPER], bv[MF::KPER];
+#pragma unroll
+    for (int j = 0; j < MF::KPER; ++j) {
+      const int k = k0 + lg * MF::KPER + j;
+      const bool kin = k < p.K;
+      av[j] = (kin && arow < p.M) ? A[(long)arow * p.lda + k] : from_f32<T>(0.f);
+      if constexpr (BT)
+        bv[j] = (kin && bcol < p.N) ? B[(long)bcol * p.ldb + k] : from_f32<T>(0.f);
+      else
+        bv[j] = (kin && bcol < p.N) ? B[(long)k * p.ldb + bcol] : from_f32<T>(0.f);
+    }
+    typename MF::frag af, bfr;
+    if constexpr (MF::KPER == 1) {
+      af = av[0];
+      bfr = bv[0];
+    } else {
+#pragma unroll
+      for (int j = 0; j < MF::KPER; ++j) {
+        af[j] = av[j];
+        bfr[j] = bv[j];
+      }
+    }
+    acc = MF::mma(af, bfr, acc);
+  }
+  const int col = tn * 32 + lr;
+  if (col >= p.N) return;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int row = tm * 32 + 8 * (e / 4) + 4 * lg + (e % 4);
+    if (row < p.M) {
+      float vv = acc[e];
+      if (R) vv += to_f32(R[(long)row * p.ldr + col]);
+      C[(long)row * p.ldc + col] = from_f32<TO>(vv);
+    }
+  }
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+template <typename T, typename TO, bool BT>
+static int gemm_dispatch(const GemmArgs& a, int batch, int variant, hipStream_t st) {
+  constexpr int E = VecE<T>::value;
+  const bool vec = aligned16(a.A) && aligned16(a.B) && a.K % E == 0 && a.lda % E == 0 && a.ldb % E == 0 &&
+                   a.sA % E == 0 && a.sB % E == 0 && (BT || a.N % E == 0);
+  if (variant == NKL_GEMM_NAIVE || !vec) {
+    const long tiles = (long)((a.M + 31) / 32) * ((a.N + 31) / 32);
+    gemm_naive_kernel<T, TO, BT><<<dim3((unsigned)((tiles + 3) / 4), 1, batch), dim3(256), 0, st>>>(a);
+    return check_launch("nkl_gemm(naive)");
+  }
+  // Largest tile that still gives every CU a workgroup; 64x64 otherwise.
+  const long t128 = (long)((a.M + 127) / 128) * ((a.N + 127) / 128) * batch;
+  const long t64x128 = (long)((a.M + 63) / 64) * ((a.N + 127) / 128) * batch;
+  if (t128 >= 256) {
+    const long tiles = (long)((a.M + 127) / 128) * ((a.N + 127) / 128);
+    gemm_blocked_kernel<T, TO, 128, 128, BT><<<dim3((unsigned)tiles, 1, batch), dim3(256), 0, st>>>(a);
+  } else if (t64x128 >= 256) {
+    const long tiles = (long)((a.M + 63) / 64) * ((a.N + 127) / 128);
+    gemm_blocked_kernel<T, TO, 64, 128, BT><<<dim3((unsigned)tiles, 1, batch), dim3(256), 0, st>>>(a);
+  } else {
+    const long tiles = (long)((a.M + 63) / 64) * ((a.N + 63) / 64);
+    gemm_blocked_kernel<T, TO, 64, 64, BT><<<dim3((unsigned)tiles, 1, batch), dim3(256), 0, st>>>(a);
+  }
+  return check_launch("nkl_gemm(blocked)");
+}
+
+template <typename T, typename TO>
+static int gemm_layout(const GemmArgs& a, int b_trans, int batch, int variant, hipStream_t st) {
+  return b_trans ? gemm_dispatch<T, TO, true>(a, batch, variant, st)
+                 : gemm_dispatch<T, TO, false>(a, batch, variant, st);
+}
+
+}  // namespace nkl
+
+using namespace nkl;
+
+extern "C" int nkl_gemm(const void* A, const void* B, void* C, const void* R, int M, int N, int K, long lda,
+                        long ldb, long ldc, long ldr, int b_trans, int batch, long strideA, long strideB,
+                        long strideC, long strideR, int dtype_in, int dtype_out, int variant, void* stream) {
+  if (M < 0 || N < 0 || K < 0 || batch < 0)
+    return set_error(NKL_EINVAL, "nkl_gemm: negative shape M=%d N=%d K=%d batch=%d", M, N, K, batch);
+  if (variant != NKL_GEMM_BLOCKED && variant != NKL_GEMM_NAIVE)
+    return set_error(NKL_EINVAL, "nkl_gemm: unknown variant %d", variant);
+  if (M == 0 || N == 0 || batch == 0) return NKL_OK;
+  if (lda < K || ldc < N || (R && ldr < N) || (b_trans ? ldb < K : ldb < N))
+    return set_error(NKL_EINVAL, "nkl_gemm: leading dimension too small (lda=%ld ldb=%ld ldc=%ld)", lda, ldb, ldc);
+  if (!A || !B || !C) return set_error(NKL_EINVAL, "nkl_gemm: null operand pointer");
+  GemmArgs a{A, B, C, R, M, N, K, lda, ldb, ldc, ldr, strideA, strideB, strideC, strideR};
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype_in == NKL_F32 && dtype_out == NKL_F32) return gemm_layout<float, float>(a, b_trans, batch, variant, st);
+  if (dtype_in == NKL_BF16 && dtype_out == NKL_BF16) return gemm_layout<bf16, bf16>(a, b_trans, batch, variant, st);
+  if (dtype_in == NKL_BF16 && dtype_out == NKL_F32) return gemm_layout<bf16, float>(a, b_trans, batch, variant, st);
+  return set_error(NKL_EDTYPE, "nkl_gemm: unsupported dtype pair (%d -> %d)", dtype_in, dtype_out);
+}
+
+extern "C" int nkl_check_blocks(int BM, int BN) {
+  if (BM < 1 || BN < 1) return set_error(NKL_EINVAL, "nkl_check_blocks: BM=%d BN=%d must be positive", BM, BN);
+  if (BM * BN > 8)
+    return set_error(NKL_ELIMIT,
+                     "BM*BN = %d fp32 [128,512] accumulators exceed the 8 PSUM banks the blocked matmul may hold",
+                     BM * BN);
+  return NKL_OK;
+}

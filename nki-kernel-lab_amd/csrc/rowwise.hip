@@ -1,0 +1,402 @@
+// Row-wise kernels: fused softmax, three-pass softmax, RMSNorm, SwiGLU.
+//
+// These are HBM-bound: every input byte is read once and every output byte
+// written once (the three-pass softmax deliberately round-trips its fp32
+// intermediates through HBM, as the reference's unfused kernel does).
+//
+// Layout: one 64-lane wavefront owns one row; a 256-thread workgroup owns 4
+// rows.  Each lane keeps NV 16-byte vectors of its row in registers, so a row
+// is read from HBM exactly once and the reductions are wavefront shuffles.
+// Rows too long for the register cache, or not 16-byte aligned, take the
+// looped kernels, which re-read the row (from L2) once per pass.
+#include <math.h>
+
+#include "common.h"
+
+namespace nkl {
+
+constexpr int kRowsPerBlock = 4;
+
+// ------------------------------------------------------------- softmax --
+// nkilab/kernels/norm.py:65-89: neg_max = -max(x); e = exp(x + neg_max) with
+// the row sum in fp32; rinv = 1 / sum; y = e * rinv rounded once.
+template <typename T, int NV>
+__global__ __launch_bounds__(256) void softmax_vec_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                          int rows, int cols, long ldx, long ldy) {
+  constexpr int E = VecE<T>::value;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + (long)row * ldx;
+  T* yr = y + (long)row * ldy;
+  const int nvec = cols / E;
+  float v[NV][E];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int n = 0; n < NV; ++n) {
+    const int vi = n * kWave + lane;
+    if (vi < nvec) {
+      load16(xr + (long)vi * E, v[n]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < E; ++e) v[n][e] = -INFINITY;
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) mx = fmaxf(mx, v[n][e]);
+  }
+  mx = wave_max(mx);
+  const float mx2 = mx * kLog2e;
+  float sum = 0.f;
+#pragma unroll
+  for (int n = 0; n < NV; ++n)
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      v[n][e] = fast_exp2(fmaf(v[n][e], kLog2e, -mx2));
+      sum += v[n][e];
+    }
+  sum = wave_sum(sum);
+  const float rinv = 1.0f / sum;
+#pragma unroll
+  for (int n = 0; n < NV; ++n) {
+    const int vi = n * kWave + lane;
+    if (vi < nvec) {
+      float o[E];
+#pragma unroll
+      for (int e = 0; e < E; ++e) o[e] = v[n][e] * rinv;
+      store_vec<E>(yr + (long)vi * E, o);
+    }
+  }
+}
+
+// Any length / alignment: one wavefront per row, three sweeps over the row.
+template <typename T>
+__global__ __launch_bounds__(256) void softmax_loop_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                           int rows, int cols, long ldx, long ldy) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + (long)row * ldx;
+  T* yr = y + (long)row * ldy;
+  float mx = -INFINITY;
+  for (int c = lane; c < cols; c += kWave) mx = fmaxf(mx, to_f32(xr[c]));
+  mx = wave_max(mx);
+  const float mx2 = mx * kLog2e;
+  float sum = 0.f;
+  for (int c = lane; c < cols; c += kWave) sum += fast_exp2(fmaf(to_f32(xr[c]), kLog2e, -mx2));
+  sum = wave_sum(sum);
+  const float rinv = 1.0f / sum;
+  for (int c = lane; c < cols; c += kWave)
+    yr[c] = from_f32<T>(fast_exp2(fmaf(to_f32(xr[c]), kLog2e, -mx2)) * rinv);
+}
+
+// ---------------------------------------------------- three-pass softmax --
+// nkilab/kernels/norm.py:22-62.  Pass 1: m = max(x) -> HBM.  Pass 2:
+// e = exp(x - m) (fp32, -> HBM) and s = sum(e) -> HBM.  Pass 3: y = e / s.
+template <typename T>
+__global__ __launch_bounds__(256) void softmax_pass1_kernel(const T* __restrict__ x, float* __restrict__ m,
+                                                            int rows, int cols, long ldx) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + (long)row * ldx;
+  float mx = -INFINITY;
+  for (int c = lane; c < cols; c += kWave) mx = fmaxf(mx, to_f32(xr[c]));
+  mx = wave_max(mx);
+  if (lane == 0) m[row] = mx;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void softmax_pass2_kernel(const T* __restrict__ x, const float* __restrict__ m,
+                                                            float* __restrict__ e, float* __restrict__ s,
+                                                            int rows, int cols, long ldx) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + (long)row * ldx;
+  float* er = e + (long)row * cols;
+  const float mr = m[row];
+  float sum = 0.f;
+  for (int c = lane; c < cols; c += kWave) {
+    const float t = fast_exp2((to_f32(xr[c]) - mr) * kLog2e);
+    er[c] = t;
+    sum += t;
+  }
+  sum = wave_sum(sum);
+  if (lane == 0) s[row] = sum;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void softmax_pass3_kernel(const float* __restrict__ e, const float* __restrict__ s,
+                                                            T* __restrict__ y, int rows, int cols, long ldy) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float* er = e + (long)row * cols;
+  T* yr = y + (long)row * ldy;
+  const float sr = s[row];
+  for (int c = lane; c < cols; c += kWave) yr[c] = from_f32<T>(er[c] / sr);
+}
+
+// ------------------------------------------------------------- RMSNorm --
+// nkilab/kernels/norm.py:92-118: ssq = sum(x^2) (fp32); ms = ssq * (1/D) + eps;
+// rstd = rsqrt(ms); xn = x * rstd (fp32); y = xn * w rounded once.
+template <typename TI, typename TO, int NV>
+__global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const TI* __restrict__ x, const TI* __restrict__ w,
+                                                          TO* __restrict__ y, int rows, int cols, long ldx,
+                                                          long ldy, float inv_d, float eps) {
+  constexpr int E = VecE<TI>::value;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const TI* xr = x + (long)row * ldx;
+  TO* yr = y + (long)row * ldy;
+  const int nvec = cols / E;
+  float v[NV][E];
+  float ssq = 0.f;
+#pragma unroll
+  for (int n = 0; n < NV; ++n) {
+    const int vi = n * kWave + lane;
+    if (vi < nvec) {
+      load16(xr + (long)vi * E, v[n]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < E; ++e) v[n][e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) ssq = fmaf(v[n][e], v[n][e], ssq);
+  }
+  ssq = wave_sum(ssq);
+  const float rstd = __frsqrt_rn(fmaf(ssq, inv_d, eps));
+#pragma unroll
+  for (int n = 0; n < NV; ++n) {
+    const int vi = n * kWave + lane;
+    if (vi < nvec) {
+      float wv[E];
+      load16(w + (long)vi * E, wv);
+      float o[E];
+#pragma unroll
+      for (int e = 0; e < E; ++e) o[e] = (v[n][e] * rstd) * wv[e];
+      store_vec<E>(yr + (long)vi * E, o);
+    }
+  }
+}
+
+template <typename TI, typename TO>
+__global__ __launch_bounds__(256) void rmsnorm_loop_kernel(const TI* __restrict__ x, const TI* __restrict__ w,
+                                                           TO* __restrict__ y, int rows, int cols, long ldx,
+                                                           long ldy, float inv_d, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const TI* xr = x + (long)row * ldx;
+  TO* yr = y + (long)row * ldy;
+  float ssq = 0.f;
+  for (int c = lane; c < cols; c += kWave) {
+    const float t = to_f32(xr[c]);
+    ssq = fmaf(t, t, ssq);
+  }
+  ssq = wave_sum(ssq);
+  const float rstd = __frsqrt_rn(fmaf(ssq, inv_d, eps));
+  for (int c = lane; c < cols; c += kWave) yr[c] = from_f32<TO>((to_f32(xr[c]) * rstd) * to_f32(w[c]));
+}
+
+// -------------------------------------------------------------- SwiGLU --
+// nkilab/kernels/norm.py:121-136: a = silu(g) in fp32; y = a * u rounded once.
+__device__ __forceinline__ float silu(float g) {
+  return g * __builtin_amdgcn_rcpf(1.0f + fast_exp2(-g * kLog2e));
+}
+
+// Each thread handles UNROLL 16-byte vectors spaced a grid-width apart.
+template <typename T, int UNROLL>
+__global__ __launch_bounds__(256) void swiglu_vec_kernel(const T* __restrict__ g, const T* __restrict__ u,
+                                                         T* __restrict__ y, long nvec) {
+  constexpr int E = VecE<T>::value;
+  const long stride = (long)gridDim.x * blockDim.x;
+  const long base = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  float gv[UNROLL][E], uv[UNROLL][E];
+#pragma unroll
+  for (int r = 0; r < UNROLL; ++r) {
+    const long vi = base + r * stride;
+    if (vi < nvec) {
+      load16(g + vi * E, gv[r]);
+      load16(u + vi * E, uv[r]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < UNROLL; ++r) {
+    const long vi = base + r * stride;
+    if (vi < nvec) {
+      float o[E];
+#pragma unroll
+      for (int e = 0; e < E; ++e) o[e] = silu(gv[r][e]) * uv[r][e];
+      store_vec<E>(y + vi * E, o);
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void swiglu_tail_kernel(const T* __restrict__ g, const T* __restrict__ u,
+                                                          T* __restrict__ y, long start, long n) {
+  const long i = start + (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = from_f32<T>(silu(to_f32(g[i])) * to_f32(u[i]));
+}
+
+// ------------------------------------------------------------ dispatch --
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Smallest register-cache depth (vectors per lane) that holds a row of nvec
+// 16-byte vectors; 0 when the row is longer than the deepest variant.
+static int pick_nv(int nvec) {
+  for (int nv = 1; nv <= 16; nv *= 2)
+    if (nvec <= nv * kWave) return nv;
+  return 0;
+}
+
+template <typename T>
+static int softmax_launch(const void* x, void* y, int rows, int cols, long ldx, long ldy, hipStream_t st) {
+  constexpr int E = VecE<T>::value;
+  const dim3 grid((rows + kRowsPerBlock - 1) / kRowsPerBlock), block(256);
+  const T* xp = static_cast<const T*>(x);
+  T* yp = static_cast<T*>(y);
+  const bool vec = cols % E == 0 && ldx % E == 0 && ldy % E == 0 && aligned16(x) && aligned16(y);
+  const int nv = vec ? pick_nv(cols / E) : 0;
+  switch (nv) {
+    case 1: softmax_vec_kernel<T, 1><<<grid, block, 0, st>>>(xp, yp, rows, cols, ldx, ldy); break;
+    case 2: softmax_vec_kernel<T, 2><<<grid, block, 0, st>>>(xp, yp, rows, cols, ldx, ldy); break;
+    case 4: softmax_vec_kernel<T, 4><<<grid, block, 0, st>>>(xp, yp, rows, cols, ldx, ldy); break;
+    case 8: softmax_vec_kernel<T, 8><<<grid, block, 0, st>>>(xp, yp, rows, cols, ldx, ldy); break;
+    case 16: softmax_vec_kernel<T, 16><<<grid, block, 0, st>>>(xp, yp, rows, cols, ldx, ldy); break;
+    default: softmax_loop_kernel<T><<<grid, block, 0, st>>>(xp, yp, rows, cols, ldx, ldy); break;
+  }
+  return check_launch("nkl_softmax");
+}
+
+template <typename TI, typename TO>
+static int rmsnorm_launch(const void* x, const void* w, void* y, int rows, int cols, long ldx, long ldy,
+                          float eps, hipStream_t st) {
+  constexpr int E = VecE<TI>::value;
+  const dim3 grid((rows + kRowsPerBlock - 1) / kRowsPerBlock), block(256);
+  const TI* xp = static_cast<const TI*>(x);
+  const TI* wp = static_cast<const TI*>(w);
+  TO* yp = static_cast<TO*>(y);
+  // The multiplier 1/D is the fp32 value nearest the exact quotient.
+  const float inv_d = (float)(1.0 / (double)cols);
+  const bool out_vec = (E * sizeof(TO)) % 8 == 0;
+  const bool vec = out_vec && cols % E == 0 && ldx % E == 0 && ldy % E == 0 && aligned16(x) &&
+                   aligned16(w) && aligned16(y);
+  const int nv = vec ? pick_nv(cols / E) : 0;
+  switch (nv) {
+    case 1: rmsnorm_vec_kernel<TI, TO, 1><<<grid, block, 0, st>>>(xp, wp, yp, rows, cols, ldx, ldy, inv_d, eps); break;
+    case 2: rmsnorm_vec_kernel<TI, TO, 2><<<grid, block, 0, st>>>(xp, wp, yp, rows, cols, ldx, ldy, inv_d, eps); break;
+    case 4: rmsnorm_vec_kernel<TI, TO, 4><<<grid, block, 0, st>>>(xp, wp, yp, rows, cols, ldx, ldy, inv_d, eps); break;
+    case 8: rmsnorm_vec_kernel<TI, TO, 8><<<grid, block, 0, st>>>(xp, wp, yp, rows, cols, ldx, ldy, inv_d, eps); break;
+    case 16: rmsnorm_vec_kernel<TI, TO, 16><<<grid, block, 0, st>>>(xp, wp, yp, rows, cols, ldx, ldy, inv_d, eps); break;
+    default: rmsnorm_loop_kernel<TI, TO><<<grid, block, 0, st>>>(xp, wp, yp, rows, cols, ldx, ldy, inv_d, eps); break;
+  }
+  return check_launch("nkl_rmsnorm");
+}
+
+template <typename T>
+static int swiglu_launch(const void* g, const void* u, void* y, long n, hipStream_t st) {
+  constexpr int E = VecE<T>::value;
+  constexpr int UNROLL = 2;
+  const T* gp = static_cast<const T*>(g);
+  const T* up = static_cast<const T*>(u);
+  T* yp = static_cast<T*>(y);
+  long done = 0;
+  if (aligned16(g) && aligned16(u) && aligned16(y)) {
+    const long nvec = n / E;
+    if (nvec > 0) {
+      const long threads = (nvec + UNROLL - 1) / UNROLL;
+      const long blocks = (threads + 255) / 256;
+      swiglu_vec_kernel<T, UNROLL><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(gp, up, yp, nvec);
+    }
+    done = nvec * E;
+  }
+  if (done < n) {
+    const long rem = n - done;
+    swiglu_tail_kernel<T><<<dim3((unsigned)((rem + 255) / 256)), dim3(256), 0, st>>>(gp, up, yp, done, n);
+  }
+  return check_launch("nkl_swiglu");
+}
+
+}  // namespace nkl
+
+using namespace nkl;
+
+static int check_rows(const char* fn, int rows, int cols, long ldx, long ldy) {
+  if (rows < 0 || cols < 0) return set_error(NKL_EINVAL, "%s: negative shape (%d, %d)", fn, rows, cols);
+  if (rows > 0 && cols > 0 && (ldx < cols || ldy < cols))
+    return set_error(NKL_EINVAL, "%s: leading dimension (%ld, %ld) smaller than cols %d", fn, ldx, ldy, cols);
+  return NKL_OK;
+}
+
+extern "C" int nkl_softmax(const void* x, void* y, int rows, int cols, long ldx, long ldy, int dtype,
+                           void* stream) {
+  int rc = check_rows("nkl_softmax", rows, cols, ldx, ldy);
+  if (rc) return rc;
+  if (rows == 0 || cols == 0) return NKL_OK;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == NKL_F32) return softmax_launch<float>(x, y, rows, cols, ldx, ldy, st);
+  if (dtype == NKL_BF16) return softmax_launch<bf16>(x, y, rows, cols, ldx, ldy, st);
+  return set_error(NKL_EDTYPE, "nkl_softmax: unsupported dtype %d", dtype);
+}
+
+extern "C" size_t nkl_softmax_unfused_workspace_bytes(int rows, int cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  const size_t r = ((size_t)rows * 4 + 255) / 256 * 256;
+  return 2 * r + (size_t)rows * (size_t)cols * 4;
+}
+
+extern "C" int nkl_softmax_unfused(const void* x, void* y, void* workspace, size_t workspace_bytes, int rows,
+                                   int cols, long ldx, long ldy, int dtype, void* stream) {
+  int rc = check_rows("nkl_softmax_unfused", rows, cols, ldx, ldy);
+  if (rc) return rc;
+  if (rows == 0 || cols == 0) return NKL_OK;
+  const size_t need = nkl_softmax_unfused_workspace_bytes(rows, cols);
+  if (!workspace || workspace_bytes < need)
+    return set_error(NKL_EWORKSPACE, "nkl_softmax_unfused: workspace of %zu bytes needed, %zu given", need,
+                     workspace_bytes);
+  const size_t r = ((size_t)rows * 4 + 255) / 256 * 256;
+  float* m = static_cast<float*>(workspace);
+  float* s = reinterpret_cast<float*>(static_cast<char*>(workspace) + r);
+  float* e = reinterpret_cast<float*>(static_cast<char*>(workspace) + 2 * r);
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((rows + kRowsPerBlock - 1) / kRowsPerBlock), block(256);
+  if (dtype == NKL_F32) {
+    softmax_pass1_kernel<float><<<grid, block, 0, st>>>(static_cast<const float*>(x), m, rows, cols, ldx);
+    softmax_pass2_kernel<float><<<grid, block, 0, st>>>(static_cast<const float*>(x), m, e, s, rows, cols, ldx);
+    softmax_pass3_kernel<float><<<grid, block, 0, st>>>(e, s, static_cast<float*>(y), rows, cols, ldy);
+  } else if (dtype == NKL_BF16) {
+    softmax_pass1_kernel<bf16><<<grid, block, 0, st>>>(static_cast<const bf16*>(x), m, rows, cols, ldx);
+    softmax_pass2_kernel<bf16><<<grid, block, 0, st>>>(static_cast<const bf16*>(x), m, e, s, rows, cols, ldx);
+    softmax_pass3_kernel<bf16><<<grid, block, 0, st>>>(e, s, static_cast<bf16*>(y), rows, cols, ldy);
+  } else {
+    return set_error(NKL_EDTYPE, "nkl_softmax_unfused: unsupported dtype %d", dtype);
+  }
+  return check_launch("nkl_softmax_unfused");
+}
+
+extern "C" int nkl_rmsnorm(const void* x, const void* w, void* y, int rows, int cols, long ldx, long ldy,
+                           float eps, int dtype_in, int dtype_out, void* stream) {
+  int rc = check_rows("nkl_rmsnorm", rows, cols, ldx, ldy);
+  if (rc) return rc;
+  if (rows == 0 || cols == 0) return NKL_OK;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype_in == NKL_F32 && dtype_out == NKL_F32)
+    return rmsnorm_launch<float, float>(x, w, y, rows, cols, ldx, ldy, eps, st);
+  if (dtype_in == NKL_BF16 && dtype_out == NKL_BF16)
+    return rmsnorm_launch<bf16, bf16>(x, w, y, rows, cols, ldx, ldy, eps, st);
+  if (dtype_in == NKL_F32 && dtype_out == NKL_BF16)
+    return rmsnorm_launch<float, bf16>(x, w, y, rows, cols, ldx, ldy, eps, st);
+  return set_error(NKL_EDTYPE, "nkl_rmsnorm: unsupported dtype pair (%d -> %d)", dtype_in, dtype_out);
+}
+
+extern "C" int nkl_swiglu(const void* g, const void* u, void* y, long n, int dtype, void* stream) {
+  if (n < 0) return set_error(NKL_EINVAL, "nkl_swiglu: negative length %ld", n);
+  if (n == 0) return NKL_OK;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == NKL_F32) return swiglu_launch<float>(g, u, y, n, st);
+  if (dtype == NKL_BF16) return swiglu_launch<bf16>(g, u, y, n, st);
+  return set_error(NKL_EDTYPE, "nkl_swiglu: unsupported dtype %d", dtype);
+}

@@ -1,0 +1,149 @@
+"""A Llama-style decoder block run two ways: PyTorch eager and the HIP kernels.
+
+    x = x + Wo . causal_attention(split_heads(RMSNorm(x) . Wqkv))
+    x = x + Wd . (silu(RMSNorm(x) . Wg) * (RMSNorm(x) . Wu))
+
+Drop-in for the reference's nkilab/model.py: BlockConfig, RMSNorm and
+DecoderBlock keep the reference's fields, attribute names and eager math
+(model.py:22-67, no rotary embeddings), because callers reach into them
+(``block.norm1.weight``, ``block.wqkv``...).  ``nki_forward`` (model.py:70-89)
+runs every heavy op -- 2 RMSNorm, 5 GEMM, 1 attention, 1 SwiGLU -- on the
+gfx950 kernels.
+
+Differences from the reference's host glue, none of which changes the math:
+  * weights are used in nn.Linear's own [out, in] layout by the B^T GEMM
+    instead of being transposed and copied on every call (model.py:76-77);
+    device copies are cached per parameter version;
+  * the head split and merge are strided views fed to the attention kernel,
+    not copies (model.py:84-86);
+  * the residual adds run in the out-projection / down-projection GEMM
+    epilogues (model.py:86, :89);
+  * ``compute_dtype="bfloat16"`` runs the block in bf16 with an fp32 residual
+    stream (the GEMMs that feed the residual emit fp32).  The default keeps
+    the reference's behaviour: everything in x's dtype.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import ops
+from ._tensors import from_device, to_device
+
+
+@dataclass
+class BlockConfig:
+    d_model: int = 256
+    n_heads: int = 4
+    d_ff: int = 1024
+    eps: float = 1e-6
+
+    @property
+    def head_dim(self) -> int:
+        return self.d_model // self.n_heads
+
+
+class RMSNorm(nn.Module):
+    """x * rsqrt(mean(x^2, -1) + eps) * weight, weight initialised to ones."""
+
+    def __init__(self, d: int, eps: float):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(d))
+
+    def forward(self, x):
+        inv_rms = torch.rsqrt(x.pow(2).mean(dim=-1, keepdim=True) + self.eps)
+        return x * inv_rms * self.weight
+
+
+class DecoderBlock(nn.Module):
+    """Pre-norm decoder block in PyTorch eager: the oracle nki_forward is held to."""
+
+    def __init__(self, cfg: BlockConfig):
+        super().__init__()
+        self.cfg = cfg
+        d, f = cfg.d_model, cfg.d_ff
+        self.norm1 = RMSNorm(d, cfg.eps)
+        self.norm2 = RMSNorm(d, cfg.eps)
+        self.wqkv = nn.Linear(d, 3 * d, bias=False)
+        self.wo = nn.Linear(d, d, bias=False)
+        self.wg = nn.Linear(d, f, bias=False)
+        self.wu = nn.Linear(d, f, bias=False)
+        self.wd = nn.Linear(f, d, bias=False)
+        # Norm weights away from 1 so that a dropped weight multiply is visible.
+        with torch.no_grad():
+            for norm in (self.norm1, self.norm2):
+                norm.weight.uniform_(0.5, 1.5)
+
+    def forward(self, x):  # x: [S, d_model]
+        S, d = x.shape
+        H, hd = self.cfg.n_heads, self.cfg.head_dim
+        heads = lambda t: t.reshape(S, H, hd).transpose(0, 1)  # noqa: E731  [H, S, hd]
+        q, k, v = (heads(t) for t in self.wqkv(self.norm1(x)).chunk(3, dim=-1))
+        attn = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+        x = x + self.wo(attn.transpose(0, 1).reshape(S, d))
+        h = self.norm2(x)
+        return x + self.wd(F.silu(self.wg(h)) * self.wu(h))
+
+
+_DTYPES = {"float32": torch.float32, "bfloat16": torch.bfloat16, torch.float32: torch.float32,
+           torch.bfloat16: torch.bfloat16}
+
+
+def _device_param(block: nn.Module, name: str, p: torch.Tensor, dtype: torch.dtype, dev: torch.device):
+    """Device copy of a parameter in `dtype`, cached until the parameter changes."""
+    cache = block.__dict__.setdefault("_nkl_param_cache", {})
+    key = (name, dtype, dev)
+    stamp = (p.data_ptr(), p._version)
+    hit = cache.get(key)
+    if hit is not None and hit[0] == stamp:
+        return hit[1]
+    t = p.detach().to(device=dev, dtype=dtype).contiguous()
+    cache[key] = (stamp, t)
+    return t
+
+
+def nki_forward(block: DecoderBlock, x, attention_variant: str = "flash_pipelined", compute_dtype=None):
+    """The same block with every heavy op on the HIP kernels (model.py:70-89).
+
+    x: [S, d_model] as NumPy or torch (CPU or GPU); returns the same kind.
+    compute_dtype: None (= x's dtype, the reference's behaviour) or "bfloat16"
+    for bf16 GEMM/attention operands with the residual stream kept in x's
+    dtype.
+    """
+    cfg = block.cfg
+    xt, kind = to_device(x)
+    dev = xt.device
+    S, d = xt.shape
+    H, hd = cfg.n_heads, cfg.head_dim
+    rdt = xt.dtype
+    cdt = rdt if compute_dtype is None else _DTYPES[compute_dtype]
+    if cdt == torch.float32 and rdt == torch.bfloat16:
+        raise ValueError("nki_forward: fp32 compute on a bf16 residual stream is not supported")
+    W = {n: _device_param(block, n, getattr(block, n).weight, cdt, dev) for n in ("wqkv", "wo", "wg", "wu", "wd")}
+    g1 = _device_param(block, "norm1", block.norm1.weight, rdt, dev)
+    g2 = _device_param(block, "norm2", block.norm2.weight, rdt, dev)
+
+    h = torch.empty((S, d), dtype=cdt, device=dev)
+    ops.rmsnorm_into(xt, g1, h, cfg.eps)
+    qkv = torch.empty((S, 3 * d), dtype=cdt, device=dev)
+    ops.linear_into(h, W["wqkv"], qkv)
+    q, k, v = (qkv[:, i * d:(i + 1) * d].view(S, H, hd).transpose(0, 1) for i in range(3))
+    a = torch.empty((S, d), dtype=cdt, device=dev)
+    ops.attention_into(q, k, v, a.view(S, H, hd).transpose(0, 1), variant=attention_variant)
+    x1 = torch.empty((S, d), dtype=rdt, device=dev)
+    ops.linear_into(a, W["wo"], x1, residual=xt)
+    h2 = torch.empty((S, d), dtype=cdt, device=dev)
+    ops.rmsnorm_into(x1, g2, h2, cfg.eps)
+    gate = torch.empty((S, cfg.d_ff), dtype=cdt, device=dev)
+    up = torch.empty((S, cfg.d_ff), dtype=cdt, device=dev)
+    ops.linear_into(h2, W["wg"], gate)
+    ops.linear_into(h2, W["wu"], up)
+    act = torch.empty((S, cfg.d_ff), dtype=cdt, device=dev)
+    ops.swiglu_into(gate, up, act)
+    out = torch.empty((S, d), dtype=rdt, device=dev)
+    ops.linear_into(act, W["wd"], out, residual=x1)
+    return from_device(out, kind)

@@ -1,0 +1,284 @@
+"""Host-side wrappers: layout, padding and tile choice around the HIP kernels.
+
+Drop-in for the reference's nkilab/ops.py: same names, signatures, argument
+meaning, output dtype (= input dtype) and errors.  Every op takes NumPy arrays
+(float32, or ml_dtypes.bfloat16 when installed) or torch tensors.  NumPy in
+gives NumPy out, synchronously, as in the reference; torch GPU tensors stay on
+the GPU and the call is asynchronous on torch's current HIP stream.
+
+Where the reference calls ``nki.simulate(kernel)(...)`` (ops.py:48-90), these
+wrappers call the C ABI of libnkilab_hip.so (include/nkilab_hip.h).  There is
+no CPU fallback: without the library or a GPU the ops raise.
+
+The ``*_into`` functions are the GPU-tensor layer underneath: they write into
+a caller-provided output, accept strided views and never copy weights, and are
+what nkilab.model uses.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._tensors import dtype_code, from_device, ptr, stream_handle, to_device, workspace
+
+# Reference tile sizes (nkilab/kernels/matmul.py:19-21, attention.py:24).  They
+# define choose_blocks' grid and _pad_to's semantics; the HIP kernels handle
+# ragged shapes themselves and never need host padding.
+TK, TM, TN = 128, 128, 512
+T = 128
+
+
+def _pad_to(x: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """Zero-pad a 2-D array at the end of both axes (ops.py:19-24)."""
+    if x.shape == (rows, cols):
+        return np.ascontiguousarray(x)
+    out = np.zeros((rows, cols), dtype=x.dtype)
+    out[: x.shape[0], : x.shape[1]] = x
+    return out
+
+
+def choose_blocks(m_tiles: int, n_tiles: int) -> tuple[int, int]:
+    """Largest BM x BN accumulator block with BM*BN <= 8 that divides the tile grid;
+    among equal-size blocks the one with the larger BN (ops.py:27-35)."""
+    cands = [(bm, bn) for bm in (1, 2, 4) for bn in (1, 2, 4, 8)
+             if bm * bn <= 8 and m_tiles % bm == 0 and n_tiles % bn == 0]
+    return max(cands, key=lambda c: (c[0] * c[1], c[1]))
+
+
+# ------------------------------------------------------------------ GEMM --
+
+_MATMUL_VARIANTS = {"blocked": _lib.GEMM_BLOCKED, "naive": _lib.GEMM_NAIVE}
+
+
+def _row_major(t: torch.Tensor, cols: int) -> tuple[torch.Tensor, int]:
+    """(tensor, leading dim) with unit column stride."""
+    if t.dim() == 2 and (t.stride(1) == 1 or t.shape[1] == 1) and t.stride(0) >= cols and t.shape[0] > 0:
+        return t, t.stride(0)
+    t = t.contiguous()
+    return t, max(cols, 1)
+
+
+def _gemm(a: torch.Tensor, bmat: torch.Tensor, ldb: int, b_trans: bool, c: torch.Tensor,
+          residual: torch.Tensor | None, variant: str) -> torch.Tensor:
+    M, K = a.shape
+    N = c.shape[1]
+    a, lda = _row_major(a, K)
+    if c.dim() != 2 or (c.stride(1) != 1 and N > 1) or (M > 1 and c.stride(0) < N):
+        raise ValueError("gemm: the output must be a row-major [M, N] tensor")
+    ldc = c.stride(0) if M > 1 else max(N, 1)
+    ldr = 0
+    if residual is not None:
+        residual, ldr = _row_major(residual, N)
+    if M == 0 or N == 0:
+        return c
+    if K == 0:
+        c.copy_(residual if residual is not None else torch.zeros_like(c))
+        return c
+    _lib.call("nkl_gemm", ptr(a), ptr(bmat), ptr(c), ptr(residual), M, N, K, lda, ldb, ldc, ldr,
+              int(b_trans), 1, 0, 0, 0, 0, dtype_code(a.dtype), dtype_code(c.dtype),
+              _MATMUL_VARIANTS[variant], stream_handle())
+    return c
+
+
+def gemm_into(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, residual: torch.Tensor | None = None,
+              variant: str = "blocked") -> torch.Tensor:
+    """c = a @ b (+ residual) on the GPU; a: [M, K], b: [K, N], c: [M, N].
+    A b stored column-major (e.g. ``w.t()`` of a row-major [N, K] weight) is
+    read in place by the B^T kernel; no transpose copy is made."""
+    K, N = b.shape
+    if N > 1 and K > 1 and b.stride(0) == 1 and b.stride(1) >= K:
+        return _gemm(a, b.t(), b.stride(1), True, c, residual, variant)
+    bm, ldb = _row_major(b, N)
+    return _gemm(a, bm, ldb, False, c, residual, variant)
+
+
+def linear_into(a: torch.Tensor, w: torch.Tensor, c: torch.Tensor, residual: torch.Tensor | None = None,
+                variant: str = "blocked") -> torch.Tensor:
+    """c = a @ w^T (+ residual) for an nn.Linear-layout weight w: [N, K]."""
+    K = a.shape[1]
+    wm, ldw = _row_major(w, K)
+    return _gemm(a, wm, ldw, True, c, residual, variant)
+
+
+def matmul(a, b, variant: str = "blocked"):
+    """C = A @ B for any shapes (ops.py:38-52).  bf16 inputs accumulate in fp32 and
+    C is rounded once; the output dtype is the input dtype."""
+    M, K = a.shape
+    K2, N = b.shape
+    assert K == K2, (a.shape, b.shape)
+    if variant not in _MATMUL_VARIANTS:
+        raise ValueError(f"unknown matmul variant {variant!r}; expected one of {sorted(_MATMUL_VARIANTS)}")
+    ta, kind = to_device(a)
+    tb, _ = to_device(b)
+    if ta.dtype != tb.dtype:
+        raise TypeError(f"matmul operands must share a dtype, got {ta.dtype} and {tb.dtype}")
+    c = torch.empty((M, N), dtype=ta.dtype, device=ta.device)
+    gemm_into(ta, tb, c, variant=variant)
+    return from_device(c, kind)
+
+
+# ------------------------------------------------------------- row ops --
+
+def _as_rows(t: torch.Tensor) -> tuple[torch.Tensor, int, int, int]:
+    """View t as [rows, cols] with unit column stride: (t2d, rows, cols, ld)."""
+    cols = t.shape[-1] if t.dim() > 0 else 1
+    t2 = t.reshape(-1, cols) if t.dim() != 2 else t
+    if t2.dim() != 2 or (t2.stride(1) != 1 and cols > 1) or t2.stride(0) < cols:
+        t2 = t2.contiguous()
+    ld = t2.stride(0) if t2.shape[0] > 1 else max(cols, 1)
+    return t2, t2.shape[0], cols, max(ld, cols)
+
+
+def softmax_into(x: torch.Tensor, y: torch.Tensor, fused: bool = True) -> torch.Tensor:
+    x2, R, D, ldx = _as_rows(x)
+    y2, _, _, ldy = _as_rows(y)
+    dt = dtype_code(x2.dtype)
+    if fused:
+        _lib.call("nkl_softmax", ptr(x2), ptr(y2), R, D, ldx, ldy, dt, stream_handle())
+    else:
+        nbytes = _lib.lib().nkl_softmax_unfused_workspace_bytes(R, D)
+        ws = workspace(nbytes, x2.device)
+        _lib.call("nkl_softmax_unfused", ptr(x2), ptr(y2), ptr(ws), nbytes, R, D, ldx, ldy, dt, stream_handle())
+    if y2.data_ptr() != y.data_ptr():
+        y.copy_(y2.view_as(y))
+    return y
+
+
+def softmax(x, fused: bool = True):
+    """Row softmax over the last dim (ops.py:55-57).  fused=True: one HBM pass
+    (norm.py:65); fused=False: three passes through HBM (norm.py:22)."""
+    t, kind = to_device(x)
+    y = torch.empty(t.shape, dtype=t.dtype, device=t.device)
+    return from_device(softmax_into(t, y, fused=fused), kind)
+
+
+def rmsnorm_into(x: torch.Tensor, weight: torch.Tensor, y: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """y = x * rsqrt(mean(x^2) + eps) * weight; weight has x's dtype, y may be
+    bf16 for an fp32 x."""
+    x2, R, D, ldx = _as_rows(x)
+    if y.stride(-1) != 1 or not y.is_contiguous():
+        raise ValueError("rmsnorm_into: output must be contiguous")
+    y2 = y.view(R, D)
+    w = weight.contiguous()
+    _lib.call("nkl_rmsnorm", ptr(x2), ptr(w), ptr(y2), R, D, ldx, D, float(eps), dtype_code(x2.dtype),
+              dtype_code(y2.dtype), stream_handle())
+    return y
+
+
+def rmsnorm(x, weight, eps: float = 1e-6):
+    """y = x * rsqrt(mean(x^2, -1) + eps) * weight (ops.py:60-61)."""
+    t, kind = to_device(x)
+    w, _ = to_device(weight)
+    w = w.to(t.dtype)
+    y = torch.empty(t.shape, dtype=t.dtype, device=t.device)
+    return from_device(rmsnorm_into(t, w, y, eps), kind)
+
+
+def swiglu_into(gate: torch.Tensor, up: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+    g, u = gate.contiguous(), up.contiguous()
+    if not y.is_contiguous():
+        raise ValueError("swiglu_into: output must be contiguous")
+    _lib.call("nkl_swiglu", ptr(g), ptr(u), ptr(y), g.numel(), dtype_code(g.dtype), stream_handle())
+    return y
+
+
+def swiglu(gate, up):
+    """y = silu(gate) * up (ops.py:64-65)."""
+    g, kind = to_device(gate)
+    u, _ = to_device(up)
+    if g.shape != u.shape:
+        raise ValueError(f"swiglu: gate {tuple(g.shape)} and up {tuple(u.shape)} differ in shape")
+    if g.dtype != u.dtype:
+        raise TypeError(f"swiglu: gate and up must share a dtype, got {g.dtype} and {u.dtype}")
+    y = torch.empty(g.shape, dtype=g.dtype, device=g.device)
+    return from_device(swiglu_into(g, u, y), kind)
+
+
+# ------------------------------------------------------------ attention --
+
+@dataclass(frozen=True)
+class AttentionVariant:
+    """One entry of ATTENTION_VARIANTS: which HIP path serves a reference variant."""
+    name: str
+    path: str          # "flash" (nkl_flash_attn_causal) or "naive" (nkl_attention_naive)
+    reference: str     # the reference kernel it stands for
+
+
+# The reference's four flash kernels differ only in Trainium engine scheduling
+# and are numerically the same online-softmax recurrence; on gfx950 one flash
+# kernel serves all four (so they agree bitwise).  "naive" keeps the unfused
+# three-pass structure with scores and probabilities in HBM.
+ATTENTION_VARIANTS = {
+    "naive": AttentionVariant("naive", "naive", "attention.py:35 attention_naive"),
+    "flash": AttentionVariant("flash", "flash", "attention.py:155 flash_attention"),
+    "flash_kv_resident": AttentionVariant("flash_kv_resident", "flash", "attention.py:179 flash_attention_kv_resident"),
+    "flash_balanced": AttentionVariant("flash_balanced", "flash", "attention.py:249 flash_attention_balanced"),
+    "flash_pipelined": AttentionVariant("flash_pipelined", "flash", "attention.py:280 flash_attention_pipelined"),
+}
+
+
+def _attn_operand(t: torch.Tensor, E: int) -> torch.Tensor:
+    ok = (t.stride(2) == 1 and t.data_ptr() % 16 == 0 and t.stride(0) % E == 0 and t.stride(1) % E == 0)
+    return t if ok else t.contiguous()
+
+
+def attention_into(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
+                   variant: str = "flash_pipelined", scale: float | None = None) -> torch.Tensor:
+    """Causal attention into o; q, k, v, o: [H, S, d] GPU tensors, any strides along
+    H and S (d contiguous).  d must be a multiple of 8 (bf16) / 4 (fp32)."""
+    spec = ATTENTION_VARIANTS[variant]
+    H, S, d = q.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    E = 8 if q.dtype == torch.bfloat16 else 4
+    q, k, v = (_attn_operand(t, E) for t in (q, k, v))
+    o_ok = o.stride(2) == 1 and o.data_ptr() % 16 == 0 and o.stride(0) % E == 0 and o.stride(1) % E == 0
+    out = o if o_ok else torch.empty((H, S, d), dtype=o.dtype, device=o.device)
+    strides = (q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
+               out.stride(0), out.stride(1))
+    dt = dtype_code(q.dtype)
+    if spec.path == "flash":
+        _lib.call("nkl_flash_attn_causal", ptr(q), ptr(k), ptr(v), ptr(out), H, S, d, *strides, float(scale), dt,
+                  stream_handle())
+    else:
+        nbytes = _lib.lib().nkl_attention_naive_workspace_bytes(H, S, dt)
+        ws = workspace(nbytes, q.device)
+        _lib.call("nkl_attention_naive", ptr(q), ptr(k), ptr(v), ptr(out), ptr(ws), nbytes, H, S, d, *strides,
+                  float(scale), dt, stream_handle())
+    if out is not o:
+        o.copy_(out)
+    return o
+
+
+def attention(q, k, v, variant: str = "flash_pipelined"):
+    """Causal attention. q, k, v: [H, S, d] (ops.py:77-91); scale 1/sqrt(d).
+
+    The reference pads S to a multiple of 128 and transposes q and k on the
+    host; the HIP kernels take [H, S, d] as is and bound-check ragged S, so
+    neither copy is made.  A head dim that is not a multiple of the 16-byte
+    vector width is zero-padded here (zeros change no dot product) and cropped.
+    """
+    spec = ATTENTION_VARIANTS[variant]  # KeyError for unknown names, as in the reference
+    tq, kind = to_device(q)
+    tk, _ = to_device(k)
+    tv, _ = to_device(v)
+    if not (tq.dtype == tk.dtype == tv.dtype):
+        raise TypeError("attention: q, k and v must share a dtype")
+    if tq.dim() != 3 or tk.shape != tq.shape or tv.shape != tq.shape:
+        raise ValueError(f"attention: q, k, v must all be [H, S, d], got {tuple(tq.shape)}, {tuple(tk.shape)}, "
+                         f"{tuple(tv.shape)}")
+    H, S, d = tq.shape
+    assert d <= 128, "head dim must be <= 128"
+    E = 8 if tq.dtype == torch.bfloat16 else 4
+    dp = -(-d // E) * E
+    if dp != d:
+        tq, tk, tv = (torch.nn.functional.pad(t, (0, dp - d)) for t in (tq, tk, tv))
+    o = torch.empty((H, S, dp), dtype=tq.dtype, device=tq.device)
+    attention_into(tq, tk, tv, o, variant=spec.name, scale=1.0 / math.sqrt(d))
+    if dp != d:
+        o = o[:, :, :d].contiguous()
+    return from_device(o, kind)

@@ -1,0 +1,118 @@
+"""GEMM kernels on the GPU against float64 products, the oracle and the golden
+fixtures (the reference's tests/test_matmul.py, plus the 1024^3 bf16 config)."""
+import numpy as np
+import pytest
+import torch
+from hypothesis import given, settings
+from hypothesis import strategies as st
+
+import oracle as O
+from conftest import assert_within_bf16_ulps, load_golden, rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf(t):
+    return torch.from_numpy(np.asarray(t, np.float32)).to(torch.bfloat16).cuda()
+
+
+def _np(t):
+    return t.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("variant", ["naive", "blocked"])
+@pytest.mark.parametrize("M,K,N", [(128, 128, 512), (256, 384, 1024), (200, 300, 130), (1, 7, 3)])
+def test_matmul_fp32(rng, variant, M, K, N):
+    from nkilab import ops
+
+    a = rng.standard_normal((M, K)).astype(np.float32)
+    b = rng.standard_normal((K, N)).astype(np.float32)
+    assert rel_err(ops.matmul(a, b, variant=variant), a.astype(np.float64) @ b) < 1e-5
+
+
+@pytest.mark.parametrize("variant", ["naive", "blocked"])
+def test_matmul_bf16_accumulates_in_fp32(rng, variant):
+    from nkilab import ops
+
+    a = _bf(rng.standard_normal((256, 1024)))
+    b = _bf(rng.standard_normal((1024, 1024)))
+    ref = _np(a).astype(np.float64) @ _np(b)
+    out = ops.matmul(a, b, variant=variant)
+    assert out.dtype == torch.bfloat16
+    assert rel_err(_np(out), ref) < 1e-2  # only the final bf16 rounding of C
+    assert_within_bf16_ulps(_np(out), O.bf16_round(ref.astype(np.float32)), 1.0, 1e-3)
+
+
+def test_matmul_1024_cubed_bf16_config():
+    """M = N = K = 1024, A and B ~ N(0, 1) bf16 from seed 0: max relative error
+    <= 3e-3 against the exact product (the bf16 rounding floor of this input is
+    2.965e-3)."""
+    from nkilab import ops, workloads
+
+    a, b = (t.cuda() for t in workloads.matmul_inputs())
+    out = _np(ops.matmul(a, b))
+    exact = _np(a).astype(np.float64) @ _np(b).astype(np.float64)
+    floor = rel_err(O.bf16_round(exact.astype(np.float32)), exact)
+    err = rel_err(out, exact)
+    assert err <= 3e-3, (err, floor)
+    assert err <= floor * 1.01 + 1e-6, (err, floor)
+    assert_within_bf16_ulps(out, O.bf16_round(exact.astype(np.float32)), 1.0, 1e-3)
+
+
+def test_matmul_matches_golden_vectors():
+    from nkilab import ops
+
+    gd = load_golden("matmul")
+    for tag, dt in (("f32", O.F32), ("f32b", O.F32), ("bf16", O.BF16)):
+        to = (lambda x: torch.from_numpy(x).cuda()) if dt == O.F32 else _bf
+        out = _np(ops.matmul(to(gd[f"{tag}_a"]), to(gd[f"{tag}_b"])))
+        ref = gd[f"{tag}_c"]
+        if dt == O.F32:
+            assert rel_err(out, ref) < 1e-5
+        else:
+            assert_within_bf16_ulps(out, ref, 1.0, 1e-3)
+
+
+@settings(max_examples=12, deadline=None)
+@given(M=st.integers(1, 300), K=st.integers(1, 300), N=st.integers(1, 700))
+def test_matmul_property_any_shape(M, K, N):
+    from nkilab import ops
+
+    r = np.random.default_rng(M * 1000003 + K * 1009 + N)
+    a = r.uniform(-1, 1, (M, K)).astype(np.float32)
+    b = r.uniform(-1, 1, (K, N)).astype(np.float32)
+    out = ops.matmul(a, b)
+    assert out.shape == (M, N)
+    np.testing.assert_allclose(out, a.astype(np.float64) @ b, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_linear_layout_and_residual_epilogue(rng, dt):
+    """C = A . W^T + R with W in nn.Linear [out, in] layout (the B^T kernel), and the
+    bf16 -> fp32 output used for the decoder's residual stream."""
+    from nkilab import ops
+
+    M, K, N = 192, 320, 256
+    a = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).to(dt).cuda()
+    w = torch.from_numpy(rng.standard_normal((N, K)).astype(np.float32)).to(dt).cuda()
+    res = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float32)).cuda()
+    c = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    ops.linear_into(a, w, c, residual=res)
+    ref = _np(a).astype(np.float64) @ _np(w).astype(np.float64).T + _np(res)
+    assert rel_err(_np(c), ref) < 1e-5
+    # the same product through gemm_into with b = w.t() (a column-major view)
+    c2 = torch.empty((M, N), dtype=dt, device="cuda")
+    ops.gemm_into(a, w.t(), c2)
+    tol = 1e-5 if dt == torch.float32 else 1e-2
+    assert rel_err(_np(c2), ref - _np(res)) < tol
+
+
+def test_nonaligned_leading_dimensions(rng):
+    from nkilab import ops
+
+    base_a = torch.from_numpy(rng.standard_normal((100, 77)).astype(np.float32)).cuda()
+    base_b = torch.from_numpy(rng.standard_normal((61, 90)).astype(np.float32)).cuda()
+    a, b = base_a[:, :61], base_b[:, :45]  # lda 77, ldb 90, K 61: the general-stride kernel
+    c = ops.matmul(a, b)
+    ref = _np(a).astype(np.float64) @ _np(b)
+    assert rel_err(_np(c), ref) < 1e-5

@@ -1,0 +1,84 @@
+"""The decoder block end to end on the HIP kernels (the reference's
+tests/test_model.py, plus the 2048-hidden bf16 block)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from conftest import load_golden, rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("S", [128, 300])
+@pytest.mark.parametrize("variant", ["naive", "flash_pipelined"])
+def test_decoder_block_matches_pytorch(S, variant):
+    from nkilab.model import BlockConfig, DecoderBlock, nki_forward
+
+    torch.manual_seed(0)
+    block = DecoderBlock(BlockConfig()).eval()
+    x = torch.randn(S, block.cfg.d_model)
+    with torch.no_grad():
+        ref = block(x).numpy()
+    out = nki_forward(block, x.numpy(), attention_variant=variant)
+    assert isinstance(out, np.ndarray) and out.dtype == np.float32
+    np.testing.assert_allclose(out, ref, atol=1e-5)
+
+
+def test_decoder_matches_golden_vectors():
+    from nkilab.model import BlockConfig, DecoderBlock, nki_forward
+
+    gd = load_golden("decoder")
+    d, f = gd["wqkv"].shape[1], gd["wg"].shape[0]
+    block = DecoderBlock(BlockConfig(d_model=d, n_heads=int(gd["n_heads"]), d_ff=f)).eval()
+    with torch.no_grad():
+        for n in ("wqkv", "wo", "wg", "wu", "wd", "norm1", "norm2"):
+            getattr(block, n).weight.copy_(torch.from_numpy(gd[n]))
+    out = nki_forward(block, gd["x"])
+    np.testing.assert_allclose(out, gd["y"], atol=1e-5)
+
+
+def test_weight_cache_follows_parameter_updates():
+    from nkilab.model import BlockConfig, DecoderBlock, nki_forward
+
+    torch.manual_seed(3)
+    block = DecoderBlock(BlockConfig(d_model=64, n_heads=2, d_ff=128)).eval()
+    x = torch.randn(32, 64)
+    first = nki_forward(block, x.numpy())
+    with torch.no_grad():
+        block.wo.weight.mul_(2.0)
+        ref = block(x).numpy()
+    np.testing.assert_allclose(nki_forward(block, x.numpy()), ref, atol=1e-5)
+    assert np.abs(first - ref).max() > 1e-3
+
+
+def test_decoder_block_2048_hidden_bf16_config():
+    """batch 1, seq 2048, hidden 2048, 16 heads x 128, FFN 5632: bf16 GEMM and
+    attention operands with an fp32 residual stream; max relative error <= 1e-3
+    against the fp32 PyTorch block (run on the GPU in fp32) on the same weights."""
+    from nkilab import workloads
+    from nkilab.model import nki_forward
+
+    block, x = workloads.decoder_inputs()
+    block = block.cuda()
+    xg = x.cuda()
+    with torch.no_grad():
+        ref = block(xg).cpu().numpy()
+    out = nki_forward(block, xg, compute_dtype="bfloat16")
+    assert out.dtype == torch.float32 and out.is_cuda
+    err = rel_err(out.cpu().numpy(), ref)
+    assert err <= 1e-3, err
+
+
+def test_decoder_bf16_matches_oracle_composition():
+    """bf16 compute path against the oracle's composition of the same kernels (small block)."""
+    from nkilab.model import BlockConfig, DecoderBlock, nki_forward
+
+    torch.manual_seed(4)
+    cfg = BlockConfig(d_model=128, n_heads=2, d_ff=256)
+    block = DecoderBlock(cfg).eval()
+    x = O.bf16_round(torch.randn(96, 128).numpy())
+    out = nki_forward(block, torch.from_numpy(x).to(torch.bfloat16)).float().numpy()
+    params = {n: getattr(block, n).weight.detach().numpy() for n in ("wqkv", "wo", "wg", "wu", "wd", "norm1", "norm2")}
+    ref = O.nki_forward_ref(params, x, cfg.n_heads, cfg.eps, "flash_pipelined", O.BF16)
+    assert rel_err(out, ref) < 2e-2

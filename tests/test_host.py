@@ -1,0 +1,165 @@
+"""CPU-only checks of the host layer and of the C ABI's shape (no kernel launches)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "nkilab_hip.h")
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(nkl_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_abi():
+    syms = _declared_symbols()
+    for name in ("nkl_gemm", "nkl_softmax", "nkl_softmax_unfused", "nkl_rmsnorm", "nkl_swiglu",
+                 "nkl_flash_attn_causal", "nkl_attention_naive", "nkl_last_error_string", "nkl_abi_version"):
+        assert name in syms
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    from nkilab import _lib
+
+    L = _lib.lib()  # dlopen only: no HIP call is made
+    for name in _declared_symbols():
+        assert hasattr(L, name), name
+    assert set(_declared_symbols()) == set(_lib.SIGNATURES)
+    assert L.nkl_abi_version() == _lib.ABI_VERSION
+
+
+def test_abi_rejects_bad_arguments_before_launching():
+    from nkilab import _lib
+
+    L = _lib.lib()
+    assert L.nkl_gemm(None, None, None, None, -1, 4, 4, 4, 4, 4, 0, 0, 1, 0, 0, 0, 0, 0, 0, 0, None) == -1
+    assert b"negative" in L.nkl_last_error_string()
+    assert L.nkl_gemm(None, None, None, None, 4, 4, 4, 4, 4, 4, 0, 0, 1, 0, 0, 0, 0, 0, 0, 7, None) == -1
+    assert L.nkl_gemm(None, None, None, None, 4, 4, 4, 4, 4, 4, 0, 0, 1, 0, 0, 0, 0, 5, 5, 0, None) in (-1, -2)
+    assert L.nkl_softmax(None, None, 0, 16, 16, 16, 1, None) == 0  # empty: nothing to do
+    assert L.nkl_softmax(None, None, 4, 16, 8, 16, 1, None) == -1  # ld < cols
+    assert L.nkl_swiglu(None, None, None, -3, 0, None) == -1
+    assert L.nkl_rmsnorm(None, None, None, 4, 4, 4, 4, ctypes.c_float(1e-6), 1, 0, None) == -2  # bf16 -> f32
+    assert L.nkl_flash_attn_causal(None, None, None, None, 1, 16, 256, 0, 0, 0, 0, 0, 0, 0, 0,
+                                   ctypes.c_float(0.1), 1, None) == -1  # d > 128
+    assert b"head dim" in L.nkl_last_error_string()
+    assert L.nkl_attention_naive(None, None, None, None, None, 0, 1, 16, 64, 0, 0, 0, 0, 0, 0, 0, 0,
+                                 ctypes.c_float(0.1), 1, None) in (-1, -4)
+    assert L.nkl_softmax_unfused_workspace_bytes(4, 8) >= 4 * 8 * 4 + 2 * 4 * 4
+    assert L.nkl_attention_naive_workspace_bytes(2, 16, 1) >= 2 * 16 * 16 * 6
+
+
+def test_psum_block_check():
+    from nkilab import _lib
+
+    L = _lib.lib()
+    assert L.nkl_check_blocks(4, 2) == 0
+    assert L.nkl_check_blocks(3, 3) == -5
+    assert b"PSUM" in L.nkl_last_error_string()
+
+
+def test_choose_blocks_respects_psum_banks():
+    from nkilab import ops
+
+    for mt in range(1, 9):
+        for nt in range(1, 17):
+            bm, bn = ops.choose_blocks(mt, nt)
+            assert bm * bn <= 8 and mt % bm == 0 and nt % bn == 0
+    assert ops.choose_blocks(4, 4) in {(2, 4), (4, 2)}
+
+
+def test_choose_blocks_agrees_with_oracle():
+    import oracle as O
+    from nkilab import ops
+
+    for mt in range(1, 17):
+        for nt in range(1, 17):
+            assert ops.choose_blocks(mt, nt) == O.choose_blocks(mt, nt)
+
+
+def test_pad_to():
+    from nkilab import ops
+
+    x = np.arange(6, dtype=np.float32).reshape(2, 3)
+    p = ops._pad_to(x, 4, 5)
+    assert p.shape == (4, 5) and np.array_equal(p[:2, :3], x) and not p[2:].any() and not p[:, 3:].any()
+    same = ops._pad_to(x.T, 3, 2)  # right shape: only made contiguous
+    assert same.flags.c_contiguous and np.array_equal(same, x.T)
+
+
+def test_api_surface_matches_reference_names():
+    from nkilab import model, ops
+
+    for name in ("matmul", "choose_blocks", "softmax", "rmsnorm", "swiglu", "attention", "ATTENTION_VARIANTS",
+                 "_pad_to"):
+        assert hasattr(ops, name), name
+    assert list(ops.ATTENTION_VARIANTS) == ["naive", "flash", "flash_kv_resident", "flash_balanced",
+                                            "flash_pipelined"]
+    for name in ("BlockConfig", "RMSNorm", "DecoderBlock", "nki_forward"):
+        assert hasattr(model, name), name
+    cfg = model.BlockConfig()
+    assert (cfg.d_model, cfg.n_heads, cfg.d_ff, cfg.eps, cfg.head_dim) == (256, 4, 1024, 1e-6, 64)
+
+
+def test_host_validation_happens_before_the_gpu():
+    from nkilab import ops
+
+    with pytest.raises(AssertionError):
+        ops.matmul(np.zeros((2, 3), np.float32), np.zeros((4, 5), np.float32))
+    with pytest.raises(KeyError):
+        ops.attention(np.zeros((1, 4, 8), np.float32), np.zeros((1, 4, 8), np.float32),
+                      np.zeros((1, 4, 8), np.float32), variant="nope")
+    with pytest.raises(ValueError):
+        ops.matmul(np.zeros((2, 3), np.float32), np.zeros((3, 5), np.float32), variant="nope")
+
+
+def test_ops_fail_loudly_without_a_gpu():
+    import torch
+
+    from nkilab import ops
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    with pytest.raises(RuntimeError, match="GPU"):
+        ops.softmax(np.zeros((2, 3), np.float32))
+
+
+def test_decoder_block_eager_matches_closed_form():
+    """The eager DecoderBlock (the decoder oracle) against an independent float64 restatement."""
+    import torch
+
+    from nkilab.model import BlockConfig, DecoderBlock
+
+    torch.manual_seed(1)
+    cfg = BlockConfig(d_model=32, n_heads=2, d_ff=48)
+    blk = DecoderBlock(cfg).eval()
+    x = torch.randn(10, 32)
+    with torch.no_grad():
+        y = blk(x).double().numpy()
+    W = {n: getattr(blk, n).weight.detach().double().numpy() for n in ("wqkv", "wo", "wg", "wu", "wd")}
+    g1, g2 = (blk.norm1.weight.detach().double().numpy(), blk.norm2.weight.detach().double().numpy())
+    xd = x.double().numpy()
+
+    def rms(t, g):
+        return t / np.sqrt((t ** 2).mean(-1, keepdims=True) + cfg.eps) * g
+
+    qkv = rms(xd, g1) @ W["wqkv"].T
+    S, d, H, hd = 10, 32, 2, 16
+    out = np.zeros((S, d))
+    for h in range(H):
+        q, k, v = (qkv[:, i * d + h * hd:i * d + (h + 1) * hd] for i in range(3))
+        s = q @ k.T / np.sqrt(hd)
+        s[np.triu_indices(S, 1)] = -np.inf
+        p = np.exp(s - s.max(-1, keepdims=True))
+        out[:, h * hd:(h + 1) * hd] = (p / p.sum(-1, keepdims=True)) @ v
+    x1 = xd + out @ W["wo"].T
+    hh = rms(x1, g2)
+    gate = hh @ W["wg"].T
+    ref = x1 + ((gate / (1 + np.exp(-gate))) * (hh @ W["wu"].T)) @ W["wd"].T
+    np.testing.assert_allclose(y, ref, atol=1e-5)
