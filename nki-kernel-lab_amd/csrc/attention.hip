@@ -114,16 +114,14 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(AttnArgs p) {
   constexpr int V_GRP = BF ? (BN / 4) * (D / 8) : 0;
   constexpr int V_IT = BF ? (V_GRP + 255) / 256 : K_CH;
   uint4 rv[BF ? V_IT * 4 : K_CH];
-  const uint4 zero = make_uint4(0, 0, 0, 0);
-
-  auto gload = [&](int k0) {
+  auto gload = [&](int k0) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < K_CH; ++i) {
       const int c = tid + 256 * i, row = c / CPR, cc = (c % CPR) * E;
       const int key = k0 + row;
-      rk[i] = (key < S && cc < dlim) ? *reinterpret_cast<const uint4*>(K + (long)key * p.k_ss + cc) : zero;
+      rk[i] = ld16_or_zero(K, (long)key * p.k_ss + cc, key < S && cc < dlim);
       if constexpr (!BF)
-        rv[i] = (key < S && cc < dlim) ? *reinterpret_cast<const uint4*>(V + (long)key * p.v_ss + cc) : zero;
+        rv[i] = ld16_or_zero(V, (long)key * p.v_ss + cc, key < S && cc < dlim);
     }
     if constexpr (BF) {
 #pragma unroll
@@ -133,15 +131,13 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(AttnArgs p) {
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
           const int key = k0 + 4 * kg + rr;
-          rv[it * 4 + rr] = (grp < V_GRP && key < S && dc < dlim)
-                                ? *reinterpret_cast<const uint4*>(V + (long)key * p.v_ss + dc)
-                                : zero;
+          rv[it * 4 + rr] = ld16_or_zero(V, (long)key * p.v_ss + dc, grp < V_GRP && key < S && dc < dlim);
         }
       }
     }
   };
 
-  auto lstore = [&](int buf) {
+  auto lstore = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < K_CH; ++i) {
       const int c = tid + 256 * i, row = c / CPR, cc = (c % CPR) * E;

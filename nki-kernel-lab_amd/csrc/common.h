@@ -152,6 +152,15 @@ struct Mfma32<float> {
   }
 };
 
+// 16-byte load of base[off] when `ok`, zeros otherwise.  The load itself is
+// unconditional (from base[0] when !ok) so that the compiler never turns the
+// choice into a load through a pointer to a private zero vector.
+template <typename T>
+__device__ __forceinline__ uint4 ld16_or_zero(const T* base, long off, bool ok) {
+  const uint4 v = *reinterpret_cast<const uint4*>(base + (ok ? off : 0));
+  return ok ? v : make_uint4(0, 0, 0, 0);
+}
+
 // Load KPER consecutive elements as one MFMA operand fragment.
 __device__ __forceinline__ bf16x8 load_frag(const bf16* p) {
   return *reinterpret_cast<const bf16x8*>(p);

@@ -79,21 +79,19 @@ __global__ __launch_bounds__(256) void gemm_blocked_kernel(GemmArgs p) {
   const TO* R = p.R ? static_cast<const TO*>(p.R) + (long)bz * p.sR : nullptr;
 
   uint4 ra[A_CH], rb[B_CH];
-  const uint4 zero = make_uint4(0, 0, 0, 0);
-
-  auto gload = [&](int k0) {
+  auto gload = [&](int k0) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < A_CH; ++i) {
       const int c = tid + 256 * i, row = c / CPR, kc = (c % CPR) * E;
       const int gm = m0 + row, gk = k0 + kc;
-      ra[i] = (gm < p.M && gk < p.K) ? *reinterpret_cast<const uint4*>(A + (long)gm * p.lda + gk) : zero;
+      ra[i] = ld16_or_zero(A, (long)gm * p.lda + gk, gm < p.M && gk < p.K);
     }
     if constexpr (BT) {
 #pragma unroll
       for (int i = 0; i < B_CH; ++i) {
         const int c = tid + 256 * i, row = c / CPR, kc = (c % CPR) * E;
         const int gn = n0 + row, gk = k0 + kc;
-        rb[i] = (gn < p.N && gk < p.K) ? *reinterpret_cast<const uint4*>(B + (long)gn * p.ldb + gk) : zero;
+        rb[i] = ld16_or_zero(B, (long)gn * p.ldb + gk, gn < p.N && gk < p.K);
       }
     } else {
       constexpr int NCH = BN / E;  // 16-byte chunks per B row of the tile
@@ -101,12 +99,12 @@ __global__ __launch_bounds__(256) void gemm_blocked_kernel(GemmArgs p) {
       for (int i = 0; i < B_CH; ++i) {
         const int c = tid + 256 * i, kr = c / NCH, nc = (c % NCH) * E;
         const int gk = k0 + kr, gn = n0 + nc;
-        rb[i] = (gk < p.K && gn < p.N) ? *reinterpret_cast<const uint4*>(B + (long)gk * p.ldb + gn) : zero;
+        rb[i] = ld16_or_zero(B, (long)gk * p.ldb + gn, gk < p.K && gn < p.N);
       }
     }
   };
 
-  auto lstore = [&](int buf) {
+  auto lstore = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < A_CH; ++i) {
       const int c = tid + 256 * i, row = c / CPR, kc = (c % CPR) * E;
