@@ -136,6 +136,29 @@ int nkl_flash_attn_causal(const void* q, const void* k, const void* v,
                           void* stream);
 
 /*
+ * The same causal attention with caller-provided scratch, which lets the bf16
+ * kernel balance the causal triangle over every CU: query blocks may be split
+ * across workgroups and finished by the last one to arrive.
+ *   workspace: partial (max, sum, output) states of split blocks,
+ *     nkl_flash_attn_causal_workspace_bytes() bytes, no initialisation.
+ *   counters: one arrival counter per query block,
+ *     nkl_flash_attn_causal_counter_bytes() bytes.  They must be zero before
+ *     the first call; every call leaves them zero, so one zeroed array (of
+ *     the largest size needed) can serve successive calls of any shape on
+ *     one stream.  Calls that may overlap need separate arrays.
+ * Both sizes are 0 for f32, which ignores them.  Same reference lines as
+ * nkl_flash_attn_causal.
+ */
+size_t nkl_flash_attn_causal_workspace_bytes(int H, int S, int d, int dtype);
+size_t nkl_flash_attn_causal_counter_bytes(int H, int S, int dtype);
+int nkl_flash_attn_causal_ws(const void* q, const void* k, const void* v,
+                             void* o, void* workspace, size_t workspace_bytes,
+                             int* counters, size_t counter_bytes, int H, int S,
+                             int d, long q_sh, long q_ss, long k_sh, long k_ss,
+                             long v_sh, long v_ss, long o_sh, long o_ss,
+                             float scale, int dtype, void* stream);
+
+/*
  * Unfused causal attention: scores (fp32, [H, S, S]) and probabilities
  * ([H, S, S], dtype) are materialised in `workspace`, then O = P V.
  * Replaces nkilab/kernels/attention.py:35 (attention_naive), selected by

@@ -23,19 +23,10 @@
 // GEMM kernels for Q.K^T and P.V and a masked row softmax in between.
 #include <math.h>
 
-#include "common.h"
+#include "attention.h"
 
 namespace nkl {
 
-struct AttnArgs {
-  const void* q;
-  const void* k;
-  const void* v;
-  void* o;
-  int H, S, d;
-  long q_sh, q_ss, k_sh, k_ss, v_sh, v_ss, o_sh, o_ss;
-  float c;  // softmax scale * log2(e): p = exp2(s * c - m)
-};
 
 template <typename T>
 struct FlashCfg;
@@ -321,20 +312,19 @@ __global__ __launch_bounds__(256) void masked_softmax_kernel(float* __restrict__
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-template <typename T, int D>
-static void flash_launch(const AttnArgs& a, hipStream_t st) {
+template <int D>
+static void flash_f32_launch(const AttnArgs& a, hipStream_t st) {
   const int nqb = (a.S + 63) / 64;
-  flash_fwd_kernel<T, D><<<dim3((unsigned)(nqb * a.H)), dim3(256), 0, st>>>(a);
+  flash_fwd_kernel<float, D><<<dim3((unsigned)(nqb * a.H)), dim3(256), 0, st>>>(a);
 }
 
-template <typename T>
-static int flash_dispatch(const AttnArgs& a, hipStream_t st) {
+static int flash_f32_dispatch(const AttnArgs& a, hipStream_t st) {
   if (a.d <= 32)
-    flash_launch<T, 32>(a, st);
+    flash_f32_launch<32>(a, st);
   else if (a.d <= 64)
-    flash_launch<T, 64>(a, st);
+    flash_f32_launch<64>(a, st);
   else
-    flash_launch<T, 128>(a, st);
+    flash_f32_launch<128>(a, st);
   return check_launch("nkl_flash_attn_causal");
 }
 
@@ -352,9 +342,12 @@ static int check_attn(const char* fn, const void* q, const void* k, const void* 
     return set_error(NKL_EINVAL, "%s: d=%d must be a multiple of %d (pad the head dim on the host)", fn, d, E);
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
     return set_error(NKL_EINVAL, "%s: q/k/v/o must be 16-byte aligned", fn);
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < 8; ++i) {
     if (strides[i] % E != 0)
       return set_error(NKL_EINVAL, "%s: stride %ld is not a multiple of %d elements", fn, strides[i], E);
+    if (strides[i] < 0 || strides[i] > (1L << 24))
+      return set_error(NKL_EINVAL, "%s: stride %ld outside [0, 2^24]", fn, strides[i]);
+  }
   return NKL_OK;
 }
 
@@ -367,8 +360,35 @@ extern "C" int nkl_flash_attn_causal(const void* q, const void* k, const void* v
   if (H == 0 || S == 0) return NKL_OK;
   AttnArgs a{q, k, v, o, H, S, d, q_sh, q_ss, k_sh, k_ss, v_sh, v_ss, o_sh, o_ss, scale * kLog2e};
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == NKL_BF16) return flash_dispatch<bf16>(a, st);
-  return flash_dispatch<float>(a, st);
+  if (dtype == NKL_BF16) return flash_bf16_launch(a, nullptr, 0, nullptr, 0, st);
+  return flash_f32_dispatch(a, st);
+}
+
+extern "C" size_t nkl_flash_attn_causal_workspace_bytes(int H, int S, int d, int dtype) {
+  if (dtype != NKL_BF16) return 0;
+  return flash_bf16_workspace_bytes(H, S, d);
+}
+
+extern "C" size_t nkl_flash_attn_causal_counter_bytes(int H, int S, int dtype) {
+  if (dtype != NKL_BF16) return 0;
+  return flash_bf16_counter_bytes(H, S);
+}
+
+extern "C" int nkl_flash_attn_causal_ws(const void* q, const void* k, const void* v, void* o, void* workspace,
+                                        size_t workspace_bytes, int* counters, size_t counter_bytes, int H, int S,
+                                        int d, long q_sh, long q_ss, long k_sh, long k_ss, long v_sh, long v_ss,
+                                        long o_sh, long o_ss, float scale, int dtype, void* stream) {
+  const long strides[8] = {q_sh, q_ss, k_sh, k_ss, v_sh, v_ss, o_sh, o_ss};
+  int rc = check_attn("nkl_flash_attn_causal_ws", q, k, v, o, H, S, d, dtype, strides);
+  if (rc) return rc;
+  if (H == 0 || S == 0) return NKL_OK;
+  AttnArgs a{q, k, v, o, H, S, d, q_sh, q_ss, k_sh, k_ss, v_sh, v_ss, o_sh, o_ss, scale * kLog2e};
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == NKL_BF16) {
+    if (!workspace) return set_error(NKL_EWORKSPACE, "nkl_flash_attn_causal_ws: null workspace");
+    return flash_bf16_launch(a, workspace, workspace_bytes, counters, counter_bytes, st);
+  }
+  return flash_f32_dispatch(a, st);
 }
 
 extern "C" size_t nkl_attention_naive_workspace_bytes(int H, int S, int dtype) {

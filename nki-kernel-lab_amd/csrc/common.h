@@ -6,7 +6,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "../../include/nkilab_hip.h"
+#include "nkilab_hip.h"
 
 namespace nkl {
 

@@ -221,6 +221,25 @@ ATTENTION_VARIANTS = {
 }
 
 
+# Flash-attention scratch, one pair per (device, stream): a partial-state
+# workspace (no initialisation needed) and an arrival-counter array zeroed
+# once, which the kernel leaves at zero after every call.  Calls on one stream
+# run one after another, so they can share both.  Each is grown when a call
+# needs more (the counters are then re-zeroed).
+_FLASH_SCRATCH: dict = {}
+
+
+def _flash_scratch(ws_bytes: int, counter_bytes: int, dev: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
+    key = (dev, stream_handle())
+    ws, cnt = _FLASH_SCRATCH.get(key, (None, None))
+    if ws is None or ws.numel() < ws_bytes:
+        ws = torch.empty(max(ws_bytes, 1 << 20), dtype=torch.uint8, device=dev)
+    if cnt is None or cnt.numel() * 4 < counter_bytes:
+        cnt = torch.zeros(max(counter_bytes // 4, 4096), dtype=torch.int32, device=dev)
+    _FLASH_SCRATCH[key] = (ws, cnt)
+    return ws, cnt
+
+
 def _attn_operand(t: torch.Tensor, E: int) -> torch.Tensor:
     ok = (t.stride(2) == 1 and t.data_ptr() % 16 == 0 and t.stride(0) % E == 0 and t.stride(1) % E == 0)
     return t if ok else t.contiguous()
@@ -242,8 +261,14 @@ def attention_into(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.T
                out.stride(0), out.stride(1))
     dt = dtype_code(q.dtype)
     if spec.path == "flash":
-        _lib.call("nkl_flash_attn_causal", ptr(q), ptr(k), ptr(v), ptr(out), H, S, d, *strides, float(scale), dt,
-                  stream_handle())
+        nbytes = _lib.lib().nkl_flash_attn_causal_workspace_bytes(H, S, d, dt)
+        if nbytes:
+            ws, cnt = _flash_scratch(nbytes, _lib.lib().nkl_flash_attn_causal_counter_bytes(H, S, dt), q.device)
+            _lib.call("nkl_flash_attn_causal_ws", ptr(q), ptr(k), ptr(v), ptr(out), ptr(ws), ws.numel(), ptr(cnt),
+                      cnt.numel() * 4, H, S, d, *strides, float(scale), dt, stream_handle())
+        else:
+            _lib.call("nkl_flash_attn_causal", ptr(q), ptr(k), ptr(v), ptr(out), H, S, d, *strides, float(scale), dt,
+                      stream_handle())
     else:
         nbytes = _lib.lib().nkl_attention_naive_workspace_bytes(H, S, dt)
         ws = workspace(nbytes, q.device)

@@ -102,6 +102,18 @@ def test_strided_heads_layout(rng):
     assert rel_err(got, ref) < 1e-2
 
 
+def test_flash_scratch_reused_across_shapes(rng):
+    """One stream's scratch serves calls of different shapes in turn: a large call's
+    partial states must not disturb a later small call's arrival counters."""
+    from nkilab import ops
+
+    for H, S, d in [(8, 2048, 128), (1, 131, 128), (2, 96, 64), (4, 1000, 64), (1, 33, 32), (8, 2048, 128)]:
+        q, k, v = (_bf(rng.standard_normal((H, S, d))) for _ in range(3))
+        out = _np(ops.attention(q, k, v))
+        ref = _sdpa_cpu(*(_np(t) for t in (q, k, v)))
+        assert rel_err(out, ref) < 1e-2, (H, S, d)
+
+
 # ------------------------------------------------ benchmark configurations --
 
 def test_causal_attention_8x2048x128_bf16_config():
