@@ -52,6 +52,8 @@ constexpr int kBufferFlags = 0x00020000;
 // below 256, which fp32 sums and bf16 probabilities represent with the same
 // relative precision, and the final O / l is unchanged.
 constexpr float kRescaleSlack = 8.0f;
+// Smallest unit range a workgroup is given in the balanced mode.
+constexpr long kMinUnits = 16;
 
 template <int D>
 struct Layout {
@@ -154,68 +156,83 @@ __global__ __launch_bounds__(512) void flash_bf16_kernel(AttnArgs p, Work w) {
     u1 = u0 + (b == w.nqb - 1 ? w.last_nt : 4 * (b + 1));
   }
 
-  for (long u = u0; u < u1;) {
-    // ---- decode the segment: head hh, query block b, tiles [t0, t1)
-    const int hh = (int)(u / w.units_head);
-    const long r = u - (long)hh * w.units_head;
+  // A segment: head hh, query block b, tiles [t0, t1) of the block's nt tiles.
+  struct Seg {
+    int hh, b, t0, t1, nt;
+    long bstart;
+  };
+  auto decode = [&](long u) __attribute__((always_inline)) {
+    Seg sg;
+    sg.hh = (int)(u / w.units_head);
+    const long r = u - (long)sg.hh * w.units_head;
     int b = (int)((sqrtf(1.0f + 2.0f * (float)r) - 1.0f) * 0.5f);
     b = min(b, w.nqb - 1);
     while (b + 1 <= w.nqb - 1 && units_before(b + 1) <= r) ++b;
     while (b > 0 && units_before(b) > r) --b;
-    const long bstart = (long)hh * w.units_head + units_before(b);
-    const int nt_b = b == w.nqb - 1 ? w.last_nt : 4 * (b + 1);
-    const long seg_end = min(u1, bstart + nt_b);
-    const int t0 = (int)(u - bstart), t1 = (int)(seg_end - bstart);
-    u = seg_end;
-
-    const bf16* Q = static_cast<const bf16*>(p.q) + (long)hh * p.q_sh;
-    const bf16* K = static_cast<const bf16*>(p.k) + (long)hh * p.k_sh;
-    const bf16* V = static_cast<const bf16*>(p.v) + (long)hh * p.v_sh;
-    const int qw = QB * b + 32 * wq;  // this wavefront's first query
-    const int myq = qw + l32;
-
-    bf16x8 qf[NQF];
+    sg.b = b;
+    sg.bstart = (long)sg.hh * w.units_head + units_before(b);
+    sg.nt = b == w.nqb - 1 ? w.last_nt : 4 * (b + 1);
+    sg.t0 = (int)(u - sg.bstart);
+    sg.t1 = (int)(min(u1, sg.bstart + sg.nt) - sg.bstart);
+    return sg;
+  };
+  auto load_q = [&](const Seg& sg, bf16x8 (&q)[NQF]) __attribute__((always_inline)) {
+    const bf16* Q = static_cast<const bf16*>(p.q) + (long)sg.hh * p.q_sh;
+    const int qrow = QB * sg.b + 32 * wq + l32;
 #pragma unroll
     for (int f = 0; f < NQF; ++f) {
       const int dd = 16 * f + 8 * h32;
-      qf[f] = __builtin_bit_cast(bf16x8, ld16_or_zero(Q, (long)myq * p.q_ss + dd, myq < S && dd < dlim));
+      q[f] = __builtin_bit_cast(bf16x8, ld16_or_zero(Q, (long)qrow * p.q_ss + dd, qrow < S && dd < dlim));
     }
-
-    const int nit = (t1 - t0 + NT - 1) / NT;
-    auto tile_of = [&](int it) __attribute__((always_inline)) { return t0 + team + NT * it; };
-
-    auto gload = [&](int it, uint4 (&rk)[CH], uint4 (&rv)[CH]) __attribute__((always_inline)) {
-      const int tj = tile_of(it);
-      const int k0 = tj * BN;
-      const int nkeys = tj < t1 ? min(BN, S - k0) : 0;
-      const int kbytes = nkeys > 0 ? 2 * ((nkeys - 1) * (int)p.k_ss + dlim) : 0;
-      const int vbytes = nkeys > 0 ? 2 * ((nkeys - 1) * (int)p.v_ss + dlim) : 0;
-      const __amdgpu_buffer_rsrc_t rk_src =
-          __builtin_amdgcn_make_buffer_rsrc((void*)(K + (long)k0 * p.k_ss), (short)0, kbytes, kBufferFlags);
-      const __amdgpu_buffer_rsrc_t rv_src =
-          __builtin_amdgcn_make_buffer_rsrc((void*)(V + (long)k0 * p.v_ss), (short)0, vbytes, kBufferFlags);
+  };
+  // Loads of one tensor (K or V) for step `it` of team `team` within segment sg.
+  auto gload = [&](const Seg& sg, int it, const void* base, long ss, const int (&goff)[CH], uint4 (&rr)[CH])
+      __attribute__((always_inline)) {
+    const int tj = sg.t0 + team + NT * it;
+    const int k0 = tj * BN;
+    const int nkeys = tj < sg.t1 ? min(BN, S - k0) : 0;
+    const int bytes = nkeys > 0 ? 2 * ((nkeys - 1) * (int)ss + dlim) : 0;
+    const __amdgpu_buffer_rsrc_t src = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(static_cast<const bf16*>(base) + (long)sg.hh * (base == p.k ? p.k_sh : p.v_sh) + (long)k0 * ss),
+        (short)0, bytes, kBufferFlags);
+#pragma unroll
+    for (int i = 0; i < CH; ++i)
+      rr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(src, goff[i], 0, 0));
+  };
+  auto lstore = [&](int stage, const uint4 (&rk)[CH], const uint4 (&rv)[CH]) __attribute__((always_inline)) {
+    bf16* sb = team_base + stage * L::STAGE;
+    if (dlim == D) {
 #pragma unroll
       for (int i = 0; i < CH; ++i) {
-        rk[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk_src, goff_k[i], 0, 0));
-        rv[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv_src, goff_v[i], 0, 0));
+        *reinterpret_cast<uint4*>(sb + loff_k[i]) = rk[i];
+        *reinterpret_cast<uint4*>(sb + loff_v[i]) = rv[i];
       }
-    };
-    auto lstore = [&](int stage, const uint4 (&rk)[CH], const uint4 (&rv)[CH]) __attribute__((always_inline)) {
-      bf16* sb = team_base + stage * L::STAGE;
-      if (dlim == D) {
+    } else {  // head-dim columns past d (a padded head dim) are stored as zeros
 #pragma unroll
-        for (int i = 0; i < CH; ++i) {
-          *reinterpret_cast<uint4*>(sb + loff_k[i]) = rk[i];
-          *reinterpret_cast<uint4*>(sb + loff_v[i]) = rv[i];
-        }
-      } else {  // head-dim columns past d (a padded head dim) are stored as zeros
-#pragma unroll
-        for (int i = 0; i < CH; ++i) {
-          *reinterpret_cast<uint4*>(sb + loff_k[i]) = dok[i] ? rk[i] : make_uint4(0, 0, 0, 0);
-          *reinterpret_cast<uint4*>(sb + loff_v[i]) = dok[i] ? rv[i] : make_uint4(0, 0, 0, 0);
-        }
+      for (int i = 0; i < CH; ++i) {
+        *reinterpret_cast<uint4*>(sb + loff_k[i]) = dok[i] ? rk[i] : make_uint4(0, 0, 0, 0);
+        *reinterpret_cast<uint4*>(sb + loff_v[i]) = dok[i] ? rv[i] : make_uint4(0, 0, 0, 0);
       }
-    };
+    }
+  };
+
+  Seg cur = decode(u0);
+  bf16x8 qf[NQF];
+  uint4 ka[CH], va[CH], kb2[CH], vb2[CH];
+  load_q(cur, qf);
+  gload(cur, 0, p.k, p.k_ss, goff_k, ka);
+  gload(cur, 0, p.v, p.v_ss, goff_v, va);
+  gload(cur, 1, p.k, p.k_ss, goff_k, kb2);
+  gload(cur, 1, p.v, p.v_ss, goff_v, vb2);
+  lstore(0, ka, va);
+  __syncthreads();
+
+  for (;;) {
+    const int hh = cur.hh, b = cur.b, t0 = cur.t0, t1 = cur.t1, nt_b = cur.nt;
+    const long bstart = cur.bstart;
+    const int qw = QB * b + 32 * wq;  // this wavefront's first query
+    const int myq = qw + l32;
+    const int nit = (t1 - t0 + NT - 1) / NT;
 
     float m_run = -INFINITY, l_run = 0.f;
     floatx16 oacc[NDB];
@@ -224,91 +241,104 @@ __global__ __launch_bounds__(512) void flash_bf16_kernel(AttnArgs p, Work w) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) oacc[db][e] = 0.f;
 
-    auto compute = [&](int it) __attribute__((always_inline)) {
-      const int tj = tile_of(it);
+    // One pipeline step: tile `it` computes from LDS stage `it & 1`; the next
+    // step's K/V (register set rk/rv, loaded one step ago) are written to the
+    // other stage; step it + 2 is loaded into (lk, lv), its V half only after
+    // the QK^T MFMAs are issued so that the two halves' loads are spread out.
+    auto step = [&](int it, uint4 (&lk)[CH], uint4 (&lv)[CH], const uint4 (&rk)[CH], const uint4 (&rv)[CH])
+        __attribute__((always_inline)) {
+      const int tj = t0 + team + NT * it;
       const int k0 = tj * BN;
-      if (tj >= t1 || k0 > qw + 31) return;  // past the segment, or above the diagonal
+      const bool active = tj < t1 && k0 <= qw + 31;  // inside the segment and not above the diagonal
       const bf16* sb = team_base + (it & 1) * L::STAGE;
+      gload(cur, it + 2, p.k, p.k_ss, goff_k, lk);
       floatx16 sacc;
 #pragma unroll
       for (int e = 0; e < 16; ++e) sacc[e] = 0.f;
+      if (active) {
 #pragma unroll
-      for (int f = 0; f < NQF; ++f) sacc = MF::mma(load_frag(sb + kfrag_off + 16 * f), qf[f], sacc);
-
-      __builtin_amdgcn_sched_barrier(0);
-      if (k0 + BN - 1 > qw) {  // diagonal tile: mask keys after the query
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-          if (k0 + 8 * (i >> 2) + 4 * h32 + (i & 3) > myq) sacc[i] = -INFINITY;
+        for (int f = 0; f < NQF; ++f) sacc = MF::mma(load_frag(sb + kfrag_off + 16 * f), qf[f], sacc);
       }
-      float mloc = sacc[0];
+      gload(cur, it + 2, p.v, p.v_ss, goff_v, lv);
+      if (active) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (k0 + BN - 1 > qw) {  // diagonal tile: mask keys after the query
 #pragma unroll
-      for (int i = 1; i < 16; ++i) mloc = fmaxf(mloc, sacc[i]);
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave)) * c;
-      if (__builtin_amdgcn_ballot_w64(mloc > m_run + kRescaleSlack)) {
-        const float m_new = fmaxf(m_run, mloc);
-        const float corr = fast_exp2(m_run - m_new);
-        m_run = m_new;
-        l_run *= corr;
+          for (int i = 0; i < 16; ++i)
+            if (k0 + 8 * (i >> 2) + 4 * h32 + (i & 3) > myq) sacc[i] = -INFINITY;
+        }
+        float mloc = sacc[0];
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
+        for (int i = 1; i < 16; ++i) mloc = fmaxf(mloc, sacc[i]);
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave)) * c;
+        if (__builtin_amdgcn_ballot_w64(mloc > m_run + kRescaleSlack)) {
+          const float m_new = fmaxf(m_run, mloc);
+          const float corr = fast_exp2(m_run - m_new);
+          m_run = m_new;
+          l_run *= corr;
 #pragma unroll
-          for (int e = 0; e < 16; ++e) oacc[db][e] *= corr;
-      }
-      float rs = 0.f;
+          for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        sacc[i] = fast_exp2(fmaf(sacc[i], c, -m_run));
-        rs += sacc[i];
-      }
-      l_run += rs;
-      bf16x8 pf[2];
+            for (int e = 0; e < 16; ++e) oacc[db][e] *= corr;
+        }
+        float rs = 0.f;
 #pragma unroll
-      for (int uu = 0; uu < 2; ++uu)
+        for (int i = 0; i < 16; ++i) {
+          sacc[i] = fast_exp2(fmaf(sacc[i], c, -m_run));
+          rs += sacc[i];
+        }
+        l_run += rs;
+        bf16x8 pf[2];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) pf[uu][j] = (bf16)sacc[8 * uu + j];
-
-      __builtin_amdgcn_sched_barrier(0);
+        for (int uu = 0; uu < 2; ++uu)
 #pragma unroll
-      for (int db = 0; db < NDB; ++db) {
+          for (int j = 0; j < 8; ++j) pf[uu][j] = (bf16)sacc[8 * uu + j];
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int uu = 0; uu < 2; ++uu) {
-          const bf16* va = sb + vfrag_off + 16 * uu * L::LDV + 32 * db;
-          const bf16x8 a = read_vt_frag(va, va + 8 * L::LDV);
-          oacc[db] = MF::mma(a, pf[uu], oacc[db]);
+        for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+          for (int uu = 0; uu < 2; ++uu) {
+            const bf16* vaddr = sb + vfrag_off + 16 * uu * L::LDV + 32 * db;
+            const bf16x8 a = read_vt_frag(vaddr, vaddr + 8 * L::LDV);
+            oacc[db] = MF::mma(a, pf[uu], oacc[db]);
+          }
         }
       }
+      lstore((it + 1) & 1, rk, rv);
+      __syncthreads();
     };
 
-    // ---- the tile pipeline: tiles it + 1 and it + 2 are in flight while it computes
-    uint4 ka[CH], va[CH], kb2[CH], vb2[CH];
-    gload(0, ka, va);
-    gload(1, kb2, vb2);
-    lstore(0, ka, va);
-    __syncthreads();
     for (int it = 0; it < nit; it += 2) {
-      gload(it + 2, ka, va);
-      compute(it);
-      lstore(1, kb2, vb2);
-      __syncthreads();
+      step(it, ka, va, kb2, vb2);
       if (it + 1 >= nit) break;
-      gload(it + 3, kb2, vb2);
-      compute(it + 1);
-      lstore(0, ka, va);
-      __syncthreads();
+      step(it + 1, kb2, vb2, ka, va);
+    }
+
+    // ---- start fetching the next segment's Q and first two K/V tiles so their
+    // latency overlaps this segment's merge and hand-off
+    const long next_u = bstart + t1;
+    const bool more = next_u < u1;
+    Seg nxt = cur;
+    if (more) {
+      nxt = decode(next_u);
+      load_q(nxt, qf);  // this segment's Q fragments are no longer needed
+      gload(nxt, 0, p.k, p.k_ss, goff_k, ka);
+      gload(nxt, 0, p.v, p.v_ss, goff_v, va);
+      gload(nxt, 1, p.k, p.k_ss, goff_k, kb2);
+      gload(nxt, 1, p.v, p.v_ss, goff_v, vb2);
     }
 
     // ---- merge the two teams (log2-domain states) into team 0
     float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
     float* red = reinterpret_cast<float*>(smem);
     if (team > 0) {
-      float* s = red + ((team - 1) * WPT + wq) * L::SLOT;
+      float* sl = red + ((team - 1) * WPT + wq) * L::SLOT;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) s[(db * 16 + e) * 64 + lane] = oacc[db][e];
-      s[16 * NDB * 64 + lane] = m_run;
-      s[(16 * NDB + 1) * 64 + lane] = l_tot;
+        for (int e = 0; e < 16; ++e) sl[(db * 16 + e) * 64 + lane] = oacc[db][e];
+      sl[16 * NDB * 64 + lane] = m_run;
+      sl[(16 * NDB + 1) * 64 + lane] = l_tot;
     }
     __syncthreads();
 
@@ -320,11 +350,9 @@ __global__ __launch_bounds__(512) void flash_bf16_kernel(AttnArgs p, Work w) {
       const float a2 = m2 == -INFINITY ? 0.f : fast_exp2(m2 - M);
       l_tot = l_tot * a1 + l2 * a2;
 #pragma unroll
-      for (int db = 0; db < NDB; ++db) {
+      for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int e = 0; e < 16; ++e) oacc[db][e] = fmaf(get(db * 16 + e), a2, oacc[db][e] * a1);
-        __builtin_amdgcn_sched_barrier(0);
-      }
       m_run = M;
     };
     auto store_out = [&]() __attribute__((always_inline)) {
@@ -349,9 +377,9 @@ __global__ __launch_bounds__(512) void flash_bf16_kernel(AttnArgs p, Work w) {
     if (team == 0) {
 #pragma unroll 1
       for (int t = 1; t < NT; ++t) {
-        const float* s = red + ((t - 1) * WPT + wq) * L::SLOT;
-        fold(s[16 * NDB * 64 + lane], s[(16 * NDB + 1) * 64 + lane],
-             [&](int j) __attribute__((always_inline)) { return s[j * 64 + lane]; });
+        const float* sl = red + ((t - 1) * WPT + wq) * L::SLOT;
+        fold(sl[16 * NDB * 64 + lane], sl[(16 * NDB + 1) * 64 + lane],
+             [&](int j) __attribute__((always_inline)) { return sl[j * 64 + lane]; });
       }
     }
 
@@ -364,8 +392,7 @@ __global__ __launch_bounds__(512) void flash_bf16_kernel(AttnArgs p, Work w) {
     if (nparts == 1) {
       if (team == 0) store_out();
     } else {
-      const long s_ = bstart;
-      const int slot = range_start(vidx, w) >= s_ ? 0 : 1;
+      const int slot = range_start(vidx, w) >= bstart ? 0 : 1;
       float* mine = w.part + ((long)vidx * 2 + slot) * L::PART + wq * L::SLOT;
       if (team == 0) {
 #pragma unroll
@@ -391,11 +418,27 @@ __global__ __launch_bounds__(512) void flash_bf16_kernel(AttnArgs p, Work w) {
 #pragma unroll 1
           for (int v2 = vf; v2 < vf + nparts; ++v2) {
             if (v2 == vidx) continue;
-            const int slot2 = range_start(v2, w) >= s_ ? 0 : 1;
+            const int slot2 = range_start(v2, w) >= bstart ? 0 : 1;
             const float* o2 = w.part + ((long)v2 * 2 + slot2) * L::PART + wq * L::SLOT;
-            fold(__builtin_nontemporal_load(o2 + 16 * NDB * 64 + lane),
-                 __builtin_nontemporal_load(o2 + (16 * NDB + 1) * 64 + lane),
-                 [&](int j) __attribute__((always_inline)) { return __builtin_nontemporal_load(o2 + j * 64 + lane); });
+            // The part's weight first, then its output in 16-value batches whose
+            // loads are each issued together before being folded in.
+            const float m2 = o2[16 * NDB * 64 + lane], l2 = o2[(16 * NDB + 1) * 64 + lane];
+            const float M = fmaxf(m_run, m2);
+            const float a1 = m_run == -INFINITY ? 0.f : fast_exp2(m_run - M);
+            const float a2 = m2 == -INFINITY ? 0.f : fast_exp2(m2 - M);
+            l_tot = l_tot * a1 + l2 * a2;
+            m_run = M;
+            constexpr int HALF = 16;
+#pragma unroll
+            for (int h0 = 0; h0 < 16 * NDB; h0 += HALF) {
+              float buf[HALF];
+#pragma unroll
+              for (int j = 0; j < HALF; ++j) buf[j] = h0 + j < 16 * NDB ? o2[(h0 + j) * 64 + lane] : 0.f;
+#pragma unroll
+              for (int j = 0; j < HALF; ++j)
+                if (h0 + j < 16 * NDB) oacc[(h0 + j) / 16][(h0 + j) % 16] = fmaf(buf[j], a2, oacc[(h0 + j) / 16][(h0 + j) % 16] * a1);
+              __builtin_amdgcn_sched_barrier(0);
+            }
           }
           store_out();
         }
@@ -403,6 +446,10 @@ __global__ __launch_bounds__(512) void flash_bf16_kernel(AttnArgs p, Work w) {
       }
     }
     __syncthreads();  // the LDS is restaged by the next segment
+    if (!more) break;
+    cur = nxt;
+    lstore(0, ka, va);
+    __syncthreads();
   }
 }
 
@@ -421,7 +468,11 @@ static Work plan(int H, int S) {
   w.last_nt = (S - 1) / BN + 1;
   w.units_head = 2L * (w.nqb - 1) * w.nqb + w.last_nt;
   w.units = (long)H * w.units_head;
-  w.grid = (int)(w.units < cu_count() ? w.units : cu_count());
+  // One workgroup per CU, but no range shorter than kMinUnits: a short range
+  // spends most of its time filling the pipeline, and splits a query block
+  // into many parts for its last workgroup to merge.
+  const long by_size = (w.units + kMinUnits - 1) / kMinUnits;
+  w.grid = (int)(by_size < cu_count() ? by_size : cu_count());
   return w;
 }
 
