@@ -209,13 +209,145 @@ def cpu_baseline(q, k, v, gpu_out):
         model = next(ln.split(":", 1)[1].strip() for ln in open("/proc/cpuinfo") if ln.startswith("model name"))
     except Exception:  # pragma: no cover
         model = "unknown"
+    rows = cpu_rows_baseline(ncores)
     base = {"value": round(flops / sec / 1e12, 5), "unit": "TFLOP/s", "cores": blas_threads, "kind": "port",
             "sample": f"full workload {H}x{S}x{d} bf16 values, oracle flash_pipelined (NumPy fp32, 128x128 tiles), "
                       f"mean of {reps} runs, {sec:.2f} s each",
             "cpu": model,
             "torch_cpu_sdpa_fp32": {"value": round(flops / tsec / 1e12, 5), "unit": "TFLOP/s", "cores": ncores,
-                                    "sec": round(tsec, 4)}}
+                                    "sec": round(tsec, 4)},
+            "row_kernels": rows}
     return base, {"attention_rel_err_vs_oracle": parity, "attention_rel_err_vs_fp32_sdpa": sdpa_err}
+
+
+def cpu_rows_baseline(ncores: int) -> dict:
+    """Softmax / RMSNorm / SwiGLU at 4096 x 2048 on the host: the oracle's NumPy
+    restatement (one thread) and PyTorch CPU in fp32 and bf16 (all cores), in
+    GB/s of the same algorithmic bytes as the GPU kernels."""
+    import numpy as np
+    import torch
+
+    import oracle as O
+    from nkilab import workloads
+
+    x, w, gate, up = workloads.rows_inputs(4096, 2048)
+    R, D = x.shape
+    nbytes = {"softmax": 2 * R * D * 2, "rmsnorm": 2 * R * D * 2 + D * 2, "swiglu": 3 * R * D * 2}
+    xn, wn, gn, un = (t.float().numpy() for t in (x, w, gate, up))
+
+    def timed(fn, reps=3):
+        fn()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        return (time.perf_counter() - t0) / reps
+
+    out = {}
+    oracle_fns = {"softmax": lambda: O.softmax_fused(xn, O.BF16),
+                  "rmsnorm": lambda: O.rmsnorm_fused(xn, wn, 1e-6, O.BF16),
+                  "swiglu": lambda: O.swiglu_fused(gn, un, O.BF16)}
+    for dt in (torch.float32, torch.bfloat16):
+        tx, tw, tg, tu = (t.to(dt) for t in (x, w, gate, up))
+        fns = {"softmax": lambda: torch.softmax(tx, dim=-1),
+               "rmsnorm": lambda: tx * torch.rsqrt(tx.float().pow(2).mean(-1, keepdim=True) + 1e-6).to(dt) * tw,
+               "swiglu": lambda: torch.nn.functional.silu(tg) * tu}
+        for name, fn in fns.items():
+            sec = timed(fn)
+            out.setdefault(name, {})[f"torch_cpu_{str(dt).split('.')[1]}"] = {
+                "GB/s": round(nbytes[name] / sec / 1e9, 3), "sec": round(sec, 5), "cores": ncores}
+    for name, fn in oracle_fns.items():
+        sec = timed(fn, reps=2)
+        out[name]["oracle_numpy"] = {"GB/s": round(nbytes[name] / sec / 1e9, 3), "sec": round(sec, 5), "cores": 1}
+    return out
+
+
+# --------------------------------------------------------- HBM traffic --
+#
+# `traffic` in the roofline objects is HBM bytes per launch from two
+# rocprofv3 counter passes, FETCH_SIZE then WRITE_SIZE (KiB per dispatch),
+# each scaled by what the same counter reads for a plain streaming kernel
+# (torch.neg over 256 MiB of fp32: one read and one write of known size) in
+# the same pass:
+#   rocprofv3 --pmc FETCH_SIZE -d OUT -o fetch -f csv -- python3 bench.py --pmc-pass
+#   rocprofv3 --pmc WRITE_SIZE -d OUT -o write -f csv -- python3 bench.py --pmc-pass
+#   python bench.py --parse-traffic OUT/.../fetch_counter_collection.csv OUT/.../write_counter_collection.csv
+# The last step writes profiles/hbm_traffic.json, which later runs report.
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+COPY_BYTES = 256 << 20
+KERNEL_KEYS = {"attention": "flash_bf16_kernel", "softmax": "softmax_vec_kernel",
+               "rmsnorm": "rmsnorm_vec_kernel", "swiglu": "swiglu_vec_kernel", "copy": "neg_kernel"}
+
+
+def pmc_pass() -> None:
+    """Eager launches for the counter passes: the calibration copy, then each
+    benchmark kernel on rotating buffer sets (cold last-level cache, as in the
+    timed runs)."""
+    import torch
+
+    from nkilab import ops, workloads
+
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)  # one streaming read and write of COPY_BYTES each
+    del src, dst
+    q, k, v = (t.cuda() for t in workloads.attention_inputs())
+    sets = [(q.clone(), k.clone(), v.clone(), torch.empty_like(q)) for _ in range(16)]
+    for b in sets:
+        ops.attention_into(*b)
+    del sets
+    x, w, gate, up = (t.cuda() for t in workloads.rows_inputs(4096, 2048))
+    xs = [(x.clone(), torch.empty_like(x)) for _ in range(16)]
+    for b in xs:
+        ops.softmax_into(*b)
+    for b in xs:
+        ops.rmsnorm_into(b[0], w, b[1], 1e-6)
+    del xs
+    gs = [(gate.clone(), up.clone(), torch.empty_like(gate)) for _ in range(11)]
+    for b in gs:
+        ops.swiglu_into(*b)
+    torch.cuda.synchronize()
+    log("pmc pass done")
+
+
+def _counter_means(path: str) -> dict:
+    import csv
+
+    sums: dict = {}
+    with open(path) as f:
+        for row in csv.DictReader(f):
+            name = row.get("Kernel_Name") or row.get("Kernel-Name") or ""
+            val = float(row.get("Counter_Value") or row.get("Counter-Value") or 0.0)
+            for key, pat in KERNEL_KEYS.items():
+                if pat in name:
+                    n, tot = sums.get(key, (0, 0.0))
+                    sums[key] = (n + 1, tot + val)
+    return {k: tot / n for k, (n, tot) in sums.items()}
+
+
+def parse_traffic(fetch_csv: str, write_csv: str) -> dict:
+    fetch, write = _counter_means(fetch_csv), _counter_means(write_csv)
+    f_copy = fetch["copy"] * 1024 / COPY_BYTES   # counter bytes per real byte read
+    w_copy = write["copy"] * 1024 / COPY_BYTES   # counter bytes per real byte written
+    out = {"calibration": {"copy_bytes": COPY_BYTES, "fetch_kib": fetch["copy"], "write_kib": write["copy"],
+                           "fetch_factor": f_copy, "write_factor": w_copy},
+           "source": [os.path.basename(fetch_csv), os.path.basename(write_csv)]}
+    for key in ("attention", "softmax", "rmsnorm", "swiglu"):
+        if key in fetch and key in write:
+            rd = fetch[key] * 1024 / f_copy
+            wr = write[key] * 1024 / w_copy
+            out[key] = {"fetch_kib": fetch[key], "write_kib": write[key], "read_bytes": round(rd),
+                        "write_bytes": round(wr), "bytes": round(rd + wr)}
+    return out
+
+
+def load_traffic() -> dict:
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return {}
 
 
 # ------------------------------------------------------------------ main --
@@ -228,7 +360,16 @@ def main() -> int:
     ap.add_argument("--all", action="store_true", help="also the GEMM, long-context and decoder configs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--report", default=None, help="write the full result dict as JSON here")
+    ap.add_argument("--pmc-pass", action="store_true", help="eager launches for a rocprofv3 --pmc run, no timing")
+    ap.add_argument("--parse-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help=f"turn two counter-collection CSVs into {os.path.relpath(TRAFFIC_FILE, ROOT)}")
     args = ap.parse_args()
+    if args.parse_traffic:
+        t = parse_traffic(*args.parse_traffic)
+        with open(TRAFFIC_FILE, "w") as f:
+            json.dump(t, f, indent=1)
+        print(json.dumps(t))
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py measures one GPU: the kernel set has no multi-GPU path (asked for {args.gpus} GPUs).",
               file=sys.stderr)
@@ -242,6 +383,9 @@ def main() -> int:
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 1
     _lib.lib()
+    if args.pmc_pass:
+        pmc_pass()
+        return 0
     props = torch.cuda.get_device_properties(0)
     log(f"device: {props.name} CUs={props.multi_processor_count} lib={_lib.LIB_PATH}")
 
@@ -254,6 +398,7 @@ def main() -> int:
     for k, r in rows.items():
         log(f"  {k:8s} {r['us']:.2f} us  {r['GB/s']:.0f} GB/s  {100 * r['frac']:.1f}% of HBM peak")
 
+    traffic = load_traffic()
     result = {
         "metric": METRIC, "value": round(att["tflops"], 3), "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(att["us"] / 1e3, 6),
@@ -263,9 +408,10 @@ def main() -> int:
                    "H": 8, "S": 2048, "d": 128,
                    "flops_per_step": att["flops"], "flop_count": "exact causal pairs 4*H*d*S(S+1)/2",
                    "device": props.name, "cus": props.multi_processor_count},
-        "roofline": roofline("mfma", att["tflops"], "TFLOP/s"),
+        "roofline": roofline("mfma", att["tflops"], "TFLOP/s", traffic.get("attention", {}).get("bytes")),
         "row_kernels": {k: {"us": round(r["us"], 3), "GB/s": round(r["GB/s"], 1), "frac": round(r["frac"], 4),
-                            "bytes": r["bytes"], "roofline": roofline("hbm", r["GB/s"], "GB/s")}
+                            "bytes": r["bytes"],
+                            "roofline": roofline("hbm", r["GB/s"], "GB/s", traffic.get(k, {}).get("bytes"))}
                         for k, r in rows.items()},
     }
     if args.all:

@@ -146,7 +146,9 @@ int nkl_flash_attn_causal(const void* q, const void* k, const void* v,
  *     the first call; every call leaves them zero, so one zeroed array (of
  *     the largest size needed) can serve successive calls of any shape on
  *     one stream.  Calls that may overlap need separate arrays.
- * Both sizes are 0 for f32, which ignores them.  Same reference lines as
+ * Both sizes are 0 for f32, and for bf16 shapes with at least as many query
+ * blocks (H * ceil(S / 128)) as the GPU has CUs: those run as
+ * nkl_flash_attn_causal does and ignore the scratch.  Same reference lines as
  * nkl_flash_attn_causal.
  */
 size_t nkl_flash_attn_causal_workspace_bytes(int H, int S, int d, int dtype);

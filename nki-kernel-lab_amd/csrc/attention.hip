@@ -385,7 +385,9 @@ extern "C" int nkl_flash_attn_causal_ws(const void* q, const void* k, const void
   AttnArgs a{q, k, v, o, H, S, d, q_sh, q_ss, k_sh, k_ss, v_sh, v_ss, o_sh, o_ss, scale * kLog2e};
   hipStream_t st = (hipStream_t)stream;
   if (dtype == NKL_BF16) {
-    if (!workspace) return set_error(NKL_EWORKSPACE, "nkl_flash_attn_causal_ws: null workspace");
+    // Shapes that need no scratch (size 0) accept a null workspace.
+    if (!workspace && flash_bf16_workspace_bytes(H, S, d) > 0)
+      return set_error(NKL_EWORKSPACE, "nkl_flash_attn_causal_ws: null workspace");
     return flash_bf16_launch(a, workspace, workspace_bytes, counters, counter_bytes, st);
   }
   return flash_f32_dispatch(a, st);

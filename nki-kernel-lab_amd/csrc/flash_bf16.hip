@@ -33,6 +33,8 @@
 // branch, so every pipeline step issues the same loads and waits only for
 // the older register set).
 #include <math.h>
+#include <stdlib.h>
+#include <string.h>
 
 #include "attention.h"
 
@@ -462,17 +464,36 @@ static int cu_count() {
   return n;
 }
 
+// Schedule choice by a cost model in units of one unit's steady-state time
+// (about 0.66 us on MI355X), fitted to measured launches of both schedules:
+//   one workgroup per block: 10.6 + max(heaviest block, units / CUs)
+//   balanced:                45.5 + 1.44 * units per workgroup
+// The balanced schedule pays for its partial states, hand-offs and shorter
+// pipelines, so it wins only where whole blocks leave CUs idle or unevenly
+// loaded (few heads, or long blocks next to short ones).
+constexpr float kPerBlockFixed = 10.6f, kBalancedFixed = 45.5f, kBalancedPerUnit = 1.44f;
+
 static Work plan(int H, int S) {
   Work w{};
   w.nqb = (S + QB - 1) / QB;
   w.last_nt = (S - 1) / BN + 1;
   w.units_head = 2L * (w.nqb - 1) * w.nqb + w.last_nt;
   w.units = (long)H * w.units_head;
+  const int cus = cu_count();
   // One workgroup per CU, but no range shorter than kMinUnits: a short range
   // spends most of its time filling the pipeline, and splits a query block
   // into many parts for its last workgroup to merge.
   const long by_size = (w.units + kMinUnits - 1) / kMinUnits;
-  w.grid = (int)(by_size < cu_count() ? by_size : cu_count());
+  w.grid = (int)(by_size < cus ? by_size : cus);
+  const float per_cu = (float)w.units / (float)cus;
+  const float per_block = kPerBlockFixed + fmaxf((float)w.last_nt, per_cu);
+  const float balanced = kBalancedFixed + kBalancedPerUnit * (float)w.units / (float)w.grid;
+  w.streamk = balanced < per_block;
+  // NKL_FLASH_SCHEDULE=balanced|block overrides the choice (tests, tuning).
+  if (const char* force = getenv("NKL_FLASH_SCHEDULE")) {
+    if (!strcmp(force, "balanced")) w.streamk = 1;
+    if (!strcmp(force, "block")) w.streamk = 0;
+  }
   return w;
 }
 
@@ -486,12 +507,13 @@ static size_t part_floats_for(int d) {
 size_t flash_bf16_workspace_bytes(int H, int S, int d) {
   if (H <= 0 || S <= 0) return 0;
   const Work w = plan(H, S);
-  return (size_t)w.grid * 2 * part_floats_for(d) * 4;
+  return w.streamk ? (size_t)w.grid * 2 * part_floats_for(d) * 4 : 0;
 }
 
 size_t flash_bf16_counter_bytes(int H, int S) {
   if (H <= 0 || S <= 0) return 0;
-  return (size_t)H * plan(H, S).nqb * 4;
+  const Work w = plan(H, S);
+  return w.streamk ? (size_t)H * w.nqb * 4 : 0;
 }
 
 template <int D>
@@ -503,14 +525,15 @@ static void launch(const AttnArgs& a, Work w, hipStream_t st) {
 int flash_bf16_launch(const AttnArgs& a, void* workspace, size_t workspace_bytes, int* counters,
                       size_t counter_bytes, hipStream_t st) {
   Work w = plan(a.H, a.S);
-  if (workspace) {
+  if (!workspace) {
+    w.streamk = 0;
+  } else if (w.streamk) {
     const size_t need = flash_bf16_workspace_bytes(a.H, a.S, a.d);
     const size_t need_c = flash_bf16_counter_bytes(a.H, a.S);
     if (workspace_bytes < need || !counters || counter_bytes < need_c)
       return set_error(NKL_EWORKSPACE,
                        "nkl_flash_attn_causal_ws: workspace of %zu bytes and counters of %zu bytes needed, "
                        "%zu and %zu given", need, need_c, workspace_bytes, counter_bytes);
-    w.streamk = 1;
     w.part = static_cast<float*>(workspace);
     w.count = counters;
   }

@@ -114,6 +114,33 @@ def test_flash_scratch_reused_across_shapes(rng):
         assert rel_err(out, ref) < 1e-2, (H, S, d)
 
 
+@pytest.mark.parametrize("schedule", ["balanced", "block"])
+@pytest.mark.parametrize("H,S,d", [(1, 1, 64), (2, 65, 32), (3, 77, 128), (1, 300, 128), (4, 1000, 64),
+                                   (2, 1537, 128), (5, 640, 96), (1, 129, 128)])
+def test_flash_bf16_schedules(rng, monkeypatch, schedule, H, S, d):
+    """Both work schedules of the bf16 kernel (split query blocks merged by the
+    last workgroup, or one workgroup per block) on ragged S and several head dims."""
+    from nkilab import ops
+
+    monkeypatch.setenv("NKL_FLASH_SCHEDULE", schedule)
+    q, k, v = (_bf(rng.standard_normal((H, S, d))) for _ in range(3))
+    out = _np(ops.attention(q, k, v))
+    ref = _sdpa_cpu(*(_np(t) for t in (q, k, v)))
+    assert rel_err(out, ref) < 1e-2, (schedule, H, S, d)
+    np.testing.assert_allclose(out[:, 0], _np(v)[:, 0], atol=1e-2)  # query 0 sees only key 0
+
+
+@pytest.mark.parametrize("schedule", ["balanced", "block"])
+def test_flash_bf16_schedules_agree_on_config(monkeypatch, schedule):
+    """8 x 2048 x 128 under each schedule: within 3e-3 of fp32 SDPA."""
+    from nkilab import ops, workloads
+
+    monkeypatch.setenv("NKL_FLASH_SCHEDULE", schedule)
+    q, k, v = (t.cuda() for t in workloads.attention_inputs())
+    out = _np(ops.attention(q, k, v))
+    assert rel_err(out, _sdpa_cpu(*(_np(t) for t in (q, k, v)))) <= 3e-3
+
+
 # ------------------------------------------------ benchmark configurations --
 
 def test_causal_attention_8x2048x128_bf16_config():

@@ -55,6 +55,21 @@ def test_abi_rejects_bad_arguments_before_launching():
     assert L.nkl_attention_naive_workspace_bytes(2, 16, 1) >= 2 * 16 * 16 * 6
 
 
+def test_flash_scratch_sizes():
+    """Balanced (split-block) scratch only where query blocks are fewer than CUs:
+    8 x 2048 has 128 blocks of 128 queries, 32 x 16384 has 4096 (the sizes
+    assume a 256-CU device, which is what the library assumes with no GPU)."""
+    from nkilab import _lib
+
+    L = _lib.lib()
+    assert L.nkl_flash_attn_causal_workspace_bytes(8, 2048, 128, 1) > 0
+    assert L.nkl_flash_attn_causal_counter_bytes(8, 2048, 1) == 8 * 16 * 4
+    assert L.nkl_flash_attn_causal_workspace_bytes(32, 16384, 128, 1) == 0
+    assert L.nkl_flash_attn_causal_counter_bytes(32, 16384, 1) == 0
+    assert L.nkl_flash_attn_causal_workspace_bytes(8, 2048, 128, 0) == 0  # f32 needs none
+    assert L.nkl_flash_attn_causal_workspace_bytes(0, 2048, 128, 1) == 0
+
+
 def test_psum_block_check():
     from nkilab import _lib
 
