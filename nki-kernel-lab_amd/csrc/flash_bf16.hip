@@ -1,21 +1,27 @@
 // bf16 causal flash attention for gfx950 -- the hot path.
 //
-// Work decomposition.  Queries are grouped in blocks of QB = 128; keys in
-// tiles of BN = 32.  A "unit" is one (head, query block, key tile) triple with
-// the tile at or below the diagonal (tiles above it are never visited), so
-// the causal triangle of S = 2048 holds 8 x 544 units.  With a workspace the
-// units are cut into equal contiguous ranges, one per workgroup and one
-// workgroup per CU (stream-K): a workgroup walks its range as segments (one
-// segment per query block it touches), and a query block split across
-// workgroups is finished by whichever of them arrives last, which merges the
-// others' partial (max, sum, output) states from the workspace.  Without a
-// workspace every workgroup takes one whole query block, heaviest first.
+// Work decomposition.  Queries are grouped in blocks of QB (64 or 128); keys
+// in tiles of BN = 32.  A "unit" is one (head, query block, key tile) triple
+// with the tile at or below the diagonal (tiles above it are never visited).
+// The units of a head are numbered block by block, either in block order or
+// in pair order -- blocks 0, n-1, 1, n-2, ... so that consecutive pairs
+// (b, n-1-b) all hold the same number of units.  Three schedules:
+//   block     one workgroup per query block, heaviest first;
+//   pairs     one workgroup per pair of blocks (equal work everywhere);
+//   balanced  the units cut into equal contiguous ranges, one per workgroup
+//             and at most one workgroup per CU (stream-K).  A workgroup walks
+//             its range as segments (one per block it touches); a block split
+//             across workgroups is finished by whichever arrives last, which
+//             folds in the others' partial (max, sum, output) states from the
+//             workspace.  In pair order with 64-query blocks, 8 x 2048 cuts
+//             into exactly two workgroups per pair.
 //
-// Workgroup.  512 threads = 8 wavefronts = 2 teams of 4.  Wavefront q of a
+// Workgroup.  NT teams of WPT wavefronts (QB = 32 WPT).  Wavefront q of a
 // team owns queries 32 q .. 32 q + 31 of the block; team t takes the tiles
-// t, t + 2, ... of the segment, so each SIMD runs two wavefronts of different
-// teams whose MFMA and exp work interleave.  At the end of a segment the two
-// teams' states are merged through LDS.
+// t, t + NT, ... of the segment, so each SIMD runs wavefronts of different
+// teams whose MFMA and exp work interleave.  At the end of a segment the
+// teams' states are combined through LDS, each team finishing its own share
+// of the head dim.
 //
 // Per 32-key tile a wavefront computes, with 32x32x16 bf16 MFMAs,
 //     S^T[32 keys x 32 queries] = K . Q^T        (8 MFMAs for d = 128)
@@ -28,10 +34,9 @@
 // (i % 4) of the 8-byte rows addressed by lanes 4 k + i / 4, k < 4: pointing
 // lane j at V[r0 + j / 4][d0 + 4 (j % 4)] gives lane i V[r0 + k][d0 + i].
 //
-// K/V tiles are staged global -> VGPR -> LDS two tiles ahead of use through
-// bounds-checked buffer loads (out-of-range chunks read as zero with no
-// branch, so every pipeline step issues the same loads and waits only for
-// the older register set).
+// K/V tiles are staged global -> VGPR -> LDS one tile ahead of use, double
+// buffered in LDS, through bounds-checked buffer loads (out-of-range chunks
+// read as zero with no branch, so every pipeline step issues the same loads).
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -42,11 +47,7 @@ namespace nkl {
 
 namespace {
 
-constexpr int QB = 128;        // queries per block (4 wavefronts x 32)
-constexpr int BN = 32;         // keys per tile
-constexpr int WPT = 4;         // wavefronts per team
-constexpr int NT = 2;          // teams
-constexpr int TT = 64 * WPT;   // threads per team
+constexpr int BN = 32;  // keys per tile
 // Buffer-resource word 3 for raw (untyped) dword loads on gfx9-family GPUs.
 constexpr int kBufferFlags = 0x00020000;
 // The running max is only raised (and O, l rescaled) when a score exceeds it
@@ -54,32 +55,49 @@ constexpr int kBufferFlags = 0x00020000;
 // below 256, which fp32 sums and bf16 probabilities represent with the same
 // relative precision, and the final O / l is unchanged.
 constexpr float kRescaleSlack = 8.0f;
-// Smallest unit range a workgroup is given in the balanced mode.
+// Smallest unit range a workgroup is given in the balanced schedule.
 constexpr long kMinUnits = 16;
+// Cache policy of the partial-state stores and loads: SC1, coherent at device
+// scope (the same policy as an agent-scope atomic load or store).  Partial
+// states travel between workgroups on different XCDs; with every store and
+// load of them device-coherent, the hand-off needs no L2 writeback or
+// invalidate -- only each store's completion (vmcnt) before the arrival
+// atomic.
+constexpr int kDeviceCoherent = 16;
 
-template <int D>
+enum Sched { kBlock = 0, kBalanced = 1, kPairs = 2 };
+
+template <int D, int WPT, int NT>
 struct Layout {
-  static constexpr int LDK = D + 8;    // K row stride: rows 4 banks apart (16-lane b128 reads)
-  static constexpr int LDV = D + 32;   // V row stride: rows 16 banks apart (32-lane b64 transposed reads)
+  static constexpr int QB = 32 * WPT;      // queries per block
+  static constexpr int TT = 64 * WPT;      // threads per team
+  static constexpr int LDK = D + 8;        // K row stride: rows 4 banks apart (16-lane b128 reads)
+  static constexpr int LDV = D + 32;       // V row stride: rows 16 banks apart (32-lane b64 transposed reads)
   static constexpr int K_ELEMS = BN * LDK;
   static constexpr int STAGE = K_ELEMS + BN * LDV;
   static constexpr int TEAM = 2 * STAGE;
   static constexpr int TOTAL = NT * TEAM;
-  static constexpr int NDB = D / 32;                  // 32-row d blocks of O^T
-  static constexpr int SLOT = 64 * (16 * NDB + 2);    // floats per wavefront in the team merge
-  static constexpr int PART = WPT * SLOT;             // floats of one partial query-block state
-  static_assert((NT - 1) * WPT * SLOT * 4 <= TOTAL * 2, "team merge does not fit in the staging LDS");
+  static constexpr int NDB = D / 32;                       // 32-row d-blocks of O^T
+  static constexpr int OWN = NDB >= NT ? NDB / NT : 1;     // d-blocks a team finishes
+  static constexpr int NCO = 4 * NDB;                      // float4 chunks of O per lane
+  static constexpr int SLOT = 64 * 4 * (NCO + 1);          // floats of one wavefront's state
+  static constexpr int PART = WPT * SLOT;                  // floats of one partial block state
+  static constexpr int XBYTES = NT * WPT * SLOT * 4;       // team hand-over area (reuses the stages)
+  static constexpr int SMEM = TOTAL * 2 > XBYTES ? TOTAL : XBYTES / 2;  // bf16 elements of LDS
 };
 
 struct Work {
   int nqb;          // query blocks per head
-  int last_nt;      // key tiles of the last (possibly partial) query block
+  int tpb;          // key tiles added per block (QB / BN): block b has tpb (b + 1)
+  int last_nt;      // key tiles of the last (possibly partial) block
+  int paired;       // unit order: 1 pair order, 0 block order
+  int sched;        // Sched
+  int grid;         // workgroups
   long units_head;  // units per head
   long units;       // total units
-  int grid;         // workgroups
-  int streamk;      // 1: balanced unit ranges; 0: one workgroup per query block
-  float* part;      // partial states [grid][2][PART]
-  int* count;       // arrival counters [H][nqb], zero between calls
+  float* part;      // balanced: partial states [grid][2][PART]
+  int part_bytes;   // balanced: bytes of part
+  int* count;       // balanced: arrival counters [H][nqb], zero between calls
 };
 
 __device__ __forceinline__ bf16x8 read_vt_frag(const bf16* row_a, const bf16* row_b) {
@@ -92,28 +110,40 @@ __device__ __forceinline__ bf16x8 read_vt_frag(const bf16* row_a, const bf16* ro
   return __builtin_bit_cast(bf16x8, c);
 }
 
-// Units before query block b of a head: blocks b' < b are full (4 (b'+1) tiles).
-__device__ __forceinline__ long units_before(int b) { return 2L * b * (b + 1); }
+__device__ __forceinline__ int block_tiles(int b, const Work& w) {
+  return b == w.nqb - 1 ? w.last_nt : w.tpb * (b + 1);
+}
+// Block order: units of a head before block b.
+__device__ __forceinline__ long plain_before(int b, const Work& w) { return (long)w.tpb * b * (b + 1) / 2; }
+// Pair order: units of a head before pair k (blocks k and n-1-k).  Every pair
+// but the first holds tpb (n + 1) units; the first lacks the last block's
+// missing tiles (tpb n - last_nt).
+__device__ __forceinline__ long pair_before(int k, const Work& w) {
+  const long full = (long)w.tpb * (w.nqb + 1);
+  const long delta = (long)w.tpb * w.nqb - w.last_nt;
+  return k == 0 ? 0 : k * full - delta;
+}
 
 __device__ __forceinline__ long range_start(long v, const Work& w) { return v * w.units / w.grid; }
 
-// The workgroup (in range order) whose range holds unit u.
+// The workgroup (in range order) whose balanced range holds unit u.
 __device__ __forceinline__ int range_of(long u, const Work& w) {
   return (int)(((u + 1) * w.grid - 1) / w.units);
 }
 
 }  // namespace
 
-template <int D>
-__global__ __launch_bounds__(512) void flash_bf16_kernel(AttnArgs p, Work w) {
-  using L = Layout<D>;
+template <int D, int WPT, int NT>
+__global__ __launch_bounds__(64 * WPT * NT) void flash_bf16_kernel(AttnArgs p, Work w) {
+  using L = Layout<D, WPT, NT>;
   using MF = Mfma32<bf16>;
+  constexpr int QB = L::QB, TT = L::TT;
   constexpr int CPR = D / 8;                    // 16-byte chunks per K/V row
   constexpr int NCHUNK = BN * CPR;              // chunks per K (or V) tile
   constexpr int CH = (NCHUNK + TT - 1) / TT;    // chunks per team thread, per tensor
   constexpr int NQF = D / 16;                   // Q^T fragments (K = 16 per MFMA)
-  constexpr int NDB = L::NDB;
-  __shared__ bf16 smem[L::TOTAL];
+  constexpr int NDB = L::NDB, OWN = L::OWN;
+  __shared__ __align__(16) bf16 smem[L::SMEM];
   __shared__ int arrival;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -144,18 +174,22 @@ __global__ __launch_bounds__(512) void flash_bf16_kernel(AttnArgs p, Work w) {
   const int i16 = lane & 15, g2 = (lane >> 4) & 1;
   const int vfrag_off = L::K_ELEMS + (4 * h32 + (i16 >> 2)) * L::LDV + 16 * g2 + 4 * (i16 & 3);
 
-  // This workgroup's unit range.
+  // This workgroup's unit range [u0, u1).
   long u0, u1;
   int vidx = blockIdx.x;
-  if (w.streamk) {
+  if (w.sched == kBalanced) {
     if (w.grid % 8 == 0) vidx = (blockIdx.x % 8) * (w.grid / 8) + blockIdx.x / 8;  // XCD-contiguous ranges
     u0 = range_start(vidx, w);
     u1 = range_start(vidx + 1, w);
+  } else if (w.sched == kPairs) {
+    const int hh = blockIdx.x % p.H, k = blockIdx.x / p.H;
+    u0 = hh * w.units_head + pair_before(k, w);
+    u1 = 2 * k + 2 <= w.nqb ? hh * w.units_head + pair_before(k + 1, w) : (hh + 1) * w.units_head;
   } else {
     const int hh = blockIdx.x % p.H;
     const int b = w.nqb - 1 - blockIdx.x / p.H;  // heaviest first
-    u0 = hh * w.units_head + units_before(b);
-    u1 = u0 + (b == w.nqb - 1 ? w.last_nt : 4 * (b + 1));
+    u0 = hh * w.units_head + plain_before(b, w);
+    u1 = u0 + block_tiles(b, w);
   }
 
   // A segment: head hh, query block b, tiles [t0, t1) of the block's nt tiles.
@@ -167,13 +201,29 @@ __global__ __launch_bounds__(512) void flash_bf16_kernel(AttnArgs p, Work w) {
     Seg sg;
     sg.hh = (int)(u / w.units_head);
     const long r = u - (long)sg.hh * w.units_head;
-    int b = (int)((sqrtf(1.0f + 2.0f * (float)r) - 1.0f) * 0.5f);
-    b = min(b, w.nqb - 1);
-    while (b + 1 <= w.nqb - 1 && units_before(b + 1) <= r) ++b;
-    while (b > 0 && units_before(b) > r) --b;
-    sg.b = b;
-    sg.bstart = (long)sg.hh * w.units_head + units_before(b);
-    sg.nt = b == w.nqb - 1 ? w.last_nt : 4 * (b + 1);
+    long before;
+    if (w.paired) {
+      const long full = (long)w.tpb * (w.nqb + 1);
+      const long delta = (long)w.tpb * w.nqb - w.last_nt;
+      const int k = min((int)((r + delta) / full), (w.nqb - 1) / 2);
+      before = pair_before(k, w);
+      const int na = block_tiles(k, w);
+      if (r - before < na) {
+        sg.b = k;
+      } else {
+        sg.b = w.nqb - 1 - k;
+        before += na;
+      }
+    } else {
+      int b = (int)((sqrtf(1.0f + 8.0f * (float)r / (float)w.tpb) - 1.0f) * 0.5f);
+      b = max(0, min(b, w.nqb - 1));
+      while (b + 1 <= w.nqb - 1 && plain_before(b + 1, w) <= r) ++b;
+      while (b > 0 && plain_before(b, w) > r) --b;
+      sg.b = b;
+      before = plain_before(b, w);
+    }
+    sg.bstart = (long)sg.hh * w.units_head + before;
+    sg.nt = block_tiles(sg.b, w);
     sg.t0 = (int)(u - sg.bstart);
     sg.t1 = (int)(min(u1, sg.bstart + sg.nt) - sg.bstart);
     return sg;
@@ -187,16 +237,15 @@ __global__ __launch_bounds__(512) void flash_bf16_kernel(AttnArgs p, Work w) {
       q[f] = __builtin_bit_cast(bf16x8, ld16_or_zero(Q, (long)qrow * p.q_ss + dd, qrow < S && dd < dlim));
     }
   };
-  // Loads of one tensor (K or V) for step `it` of team `team` within segment sg.
-  auto gload = [&](const Seg& sg, int it, const void* base, long ss, const int (&goff)[CH], uint4 (&rr)[CH])
-      __attribute__((always_inline)) {
+  // Loads of one tensor (K or V) for step `it` of this team within segment sg.
+  auto gload = [&](const Seg& sg, int it, const void* base, long sh, long ss, const int (&goff)[CH],
+                   uint4 (&rr)[CH]) __attribute__((always_inline)) {
     const int tj = sg.t0 + team + NT * it;
     const int k0 = tj * BN;
     const int nkeys = tj < sg.t1 ? min(BN, S - k0) : 0;
     const int bytes = nkeys > 0 ? 2 * ((nkeys - 1) * (int)ss + dlim) : 0;
     const __amdgpu_buffer_rsrc_t src = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(static_cast<const bf16*>(base) + (long)sg.hh * (base == p.k ? p.k_sh : p.v_sh) + (long)k0 * ss),
-        (short)0, bytes, kBufferFlags);
+        (void*)(static_cast<const bf16*>(base) + (long)sg.hh * sh + (long)k0 * ss), (short)0, bytes, kBufferFlags);
 #pragma unroll
     for (int i = 0; i < CH; ++i)
       rr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(src, goff[i], 0, 0));
@@ -220,14 +269,10 @@ __global__ __launch_bounds__(512) void flash_bf16_kernel(AttnArgs p, Work w) {
 
   Seg cur = decode(u0);
   bf16x8 qf[NQF];
-  uint4 ka[CH], va[CH], kb2[CH], vb2[CH];
+  uint4 rk[CH], rv[CH];  // the next tile's K and V on their way to LDS
   load_q(cur, qf);
-  gload(cur, 0, p.k, p.k_ss, goff_k, ka);
-  gload(cur, 0, p.v, p.v_ss, goff_v, va);
-  gload(cur, 1, p.k, p.k_ss, goff_k, kb2);
-  gload(cur, 1, p.v, p.v_ss, goff_v, vb2);
-  lstore(0, ka, va);
-  __syncthreads();
+  gload(cur, 0, p.k, p.k_sh, p.k_ss, goff_k, rk);
+  gload(cur, 0, p.v, p.v_sh, p.v_ss, goff_v, rv);
 
   for (;;) {
     const int hh = cur.hh, b = cur.b, t0 = cur.t0, t1 = cur.t1, nt_b = cur.nt;
@@ -236,6 +281,11 @@ __global__ __launch_bounds__(512) void flash_bf16_kernel(AttnArgs p, Work w) {
     const int myq = qw + l32;
     const int nit = (t1 - t0 + NT - 1) / NT;
 
+    lstore(0, rk, rv);
+    __syncthreads();
+    gload(cur, 1, p.k, p.k_sh, p.k_ss, goff_k, rk);
+    gload(cur, 1, p.v, p.v_sh, p.v_ss, goff_v, rv);
+
     float m_run = -INFINITY, l_run = 0.f;
     floatx16 oacc[NDB];
 #pragma unroll
@@ -243,26 +293,21 @@ __global__ __launch_bounds__(512) void flash_bf16_kernel(AttnArgs p, Work w) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) oacc[db][e] = 0.f;
 
-    // One pipeline step: tile `it` computes from LDS stage `it & 1`; the next
-    // step's K/V (register set rk/rv, loaded one step ago) are written to the
-    // other stage; step it + 2 is loaded into (lk, lv), its V half only after
-    // the QK^T MFMAs are issued so that the two halves' loads are spread out.
-    auto step = [&](int it, uint4 (&lk)[CH], uint4 (&lv)[CH], const uint4 (&rk)[CH], const uint4 (&rv)[CH])
-        __attribute__((always_inline)) {
+    // Step `it`: tile it computes from LDS stage it & 1; tile it + 1 (in
+    // registers since the previous step) is written to the other stage; after
+    // the barrier tile it + 2 is loaded into the registers.
+#pragma unroll 1
+    for (int it = 0; it < nit; ++it) {
       const int tj = t0 + team + NT * it;
       const int k0 = tj * BN;
       const bool active = tj < t1 && k0 <= qw + 31;  // inside the segment and not above the diagonal
       const bf16* sb = team_base + (it & 1) * L::STAGE;
-      gload(cur, it + 2, p.k, p.k_ss, goff_k, lk);
-      floatx16 sacc;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) sacc[e] = 0.f;
       if (active) {
+        floatx16 sacc;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sacc[e] = 0.f;
 #pragma unroll
         for (int f = 0; f < NQF; ++f) sacc = MF::mma(load_frag(sb + kfrag_off + 16 * f), qf[f], sacc);
-      }
-      gload(cur, it + 2, p.v, p.v_ss, goff_v, lv);
-      if (active) {
         __builtin_amdgcn_sched_barrier(0);
         if (k0 + BN - 1 > qw) {  // diagonal tile: mask keys after the query
 #pragma unroll
@@ -308,226 +353,290 @@ __global__ __launch_bounds__(512) void flash_bf16_kernel(AttnArgs p, Work w) {
       }
       lstore((it + 1) & 1, rk, rv);
       __syncthreads();
-    };
-
-    for (int it = 0; it < nit; it += 2) {
-      step(it, ka, va, kb2, vb2);
-      if (it + 1 >= nit) break;
-      step(it + 1, kb2, vb2, ka, va);
+      gload(cur, it + 2, p.k, p.k_sh, p.k_ss, goff_k, rk);
+      gload(cur, it + 2, p.v, p.v_sh, p.v_ss, goff_v, rv);
     }
 
-    // ---- start fetching the next segment's Q and first two K/V tiles so their
-    // latency overlaps this segment's merge and hand-off
-    const long next_u = bstart + t1;
-    const bool more = next_u < u1;
-    Seg nxt = cur;
-    if (more) {
-      nxt = decode(next_u);
-      load_q(nxt, qf);  // this segment's Q fragments are no longer needed
-      gload(nxt, 0, p.k, p.k_ss, goff_k, ka);
-      gload(nxt, 0, p.v, p.v_ss, goff_v, va);
-      gload(nxt, 1, p.k, p.k_ss, goff_k, kb2);
-      gload(nxt, 1, p.v, p.v_ss, goff_v, vb2);
-    }
-
-    // ---- merge the two teams (log2-domain states) into team 0
-    float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
-    float* red = reinterpret_cast<float*>(smem);
-    if (team > 0) {
-      float* sl = red + ((team - 1) * WPT + wq) * L::SLOT;
+    // ---- hand-over between the teams.  Team t finishes d-blocks
+    // [t OWN, (t + 1) OWN) of O (teams past the last d-block finish none) and
+    // writes the other d-blocks of its state, with its (m, l), to LDS.  A
+    // wavefront's state is float4 chunk k of lane l at k * 64 + l: chunks
+    // 4 db .. 4 db + 3 hold d-block db, chunk NCO holds (m, l).
+    const int own0 = team * OWN;
+    const bool keeps = own0 < NDB;
+    float l_tot = l_run + __shfl_xor(l_run, 32, kWave);  // lanes l and l ^ 32 hold the same query
+    {
+      float4* xs = reinterpret_cast<float4*>(smem) + (team * WPT + wq) * (L::SLOT / 4) + lane;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
+        if (db / OWN != team)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) sl[(db * 16 + e) * 64 + lane] = oacc[db][e];
-      sl[16 * NDB * 64 + lane] = m_run;
-      sl[(16 * NDB + 1) * 64 + lane] = l_tot;
+          for (int k = 0; k < 4; ++k)
+            xs[(4 * db + k) * 64] =
+                make_float4(oacc[db][4 * k], oacc[db][4 * k + 1], oacc[db][4 * k + 2], oacc[db][4 * k + 3]);
+      xs[L::NCO * 64] = make_float4(m_run, l_tot, 0.f, 0.f);
     }
+    floatx16 own[OWN];  // the d-blocks this team finishes, with compile-time indices
+#pragma unroll
+    for (int j = 0; j < OWN; ++j) own[j] = oacc[j];
+#pragma unroll
+    for (int t = 1; t < NT; ++t)
+      if (team == t && t * OWN < NDB)
+#pragma unroll
+        for (int j = 0; j < OWN; ++j) own[j] = oacc[t * OWN + j < NDB ? t * OWN + j : NDB - 1];
     __syncthreads();
 
-    // Folds the state (m2, l2, O2 read via `get`) into (m_run, l_tot, oacc).
-    auto fold = [&](float m2, float l2, auto get) __attribute__((always_inline)) {
-      // An empty state has m = -inf: its weight is 0 (and two empty states stay empty).
+    // Folds a state with max m2 and sum l2 into (m_run, l_tot) and returns the
+    // weights of the running state (a1) and of the other (a2).  An empty state
+    // has m = -inf and weight 0, and two empty states stay empty.
+    auto weights = [&](float m2, float l2, float& a1, float& a2) __attribute__((always_inline)) {
       const float M = fmaxf(m_run, m2);
-      const float a1 = m_run == -INFINITY ? 0.f : fast_exp2(m_run - M);
-      const float a2 = m2 == -INFINITY ? 0.f : fast_exp2(m2 - M);
+      a1 = m_run == -INFINITY ? 0.f : fast_exp2(m_run - M);
+      a2 = m2 == -INFINITY ? 0.f : fast_exp2(m2 - M);
       l_tot = l_tot * a1 + l2 * a2;
-#pragma unroll
-      for (int db = 0; db < NDB; ++db)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) oacc[db][e] = fmaf(get(db * 16 + e), a2, oacc[db][e] * a1);
       m_run = M;
     };
+    // Folds a wavefront state whose float4 chunk k (this lane's) is get(k);
+    // all of its loads are issued before any is used.
+    auto fold_state = [&](auto get) __attribute__((always_inline)) {
+      const float4 st = get(L::NCO);
+      float4 v[OWN][4];
+      if (keeps) {
+#pragma unroll
+        for (int j = 0; j < OWN; ++j)
+#pragma unroll
+          for (int k = 0; k < 4; ++k) v[j][k] = get(4 * (own0 + j) + k);
+      }
+      float a1, a2;
+      weights(st.x, st.y, a1, a2);
+      if (keeps) {
+#pragma unroll
+        for (int j = 0; j < OWN; ++j)
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            own[j][4 * k] = fmaf(v[j][k].x, a2, own[j][4 * k] * a1);
+            own[j][4 * k + 1] = fmaf(v[j][k].y, a2, own[j][4 * k + 1] * a1);
+            own[j][4 * k + 2] = fmaf(v[j][k].z, a2, own[j][4 * k + 2] * a1);
+            own[j][4 * k + 3] = fmaf(v[j][k].w, a2, own[j][4 * k + 3] * a1);
+          }
+      }
+    };
+#pragma unroll
+    for (int t2 = 0; t2 < NT; ++t2)
+      if (t2 != team) {
+        const float4* xo = reinterpret_cast<const float4*>(smem) + (t2 * WPT + wq) * (L::SLOT / 4) + lane;
+        fold_state([&](int k) __attribute__((always_inline)) { return xo[k * 64]; });
+      }
+
+    // Writes this team's d-blocks of O / l for the wavefront's 32 queries.
     auto store_out = [&]() __attribute__((always_inline)) {
       const float linv = 1.0f / l_tot;
-      if (myq < S) {
+      if (keeps && myq < S) {
         bf16* orow = static_cast<bf16*>(p.o) + (long)hh * p.o_sh + (long)myq * p.o_ss;
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
+        for (int j = 0; j < OWN; ++j)
 #pragma unroll
           for (int bq = 0; bq < 4; ++bq) {
-            const int dd = 32 * db + 8 * bq + 4 * h32;
+            const int dd = 32 * (own0 + j) + 8 * bq + 4 * h32;
             if (dd < dlim) {
               float ov[4];
 #pragma unroll
-              for (int e = 0; e < 4; ++e) ov[e] = oacc[db][4 * bq + e] * linv;
+              for (int e = 0; e < 4; ++e) ov[e] = own[j][4 * bq + e] * linv;
               store_vec<4>(orow + dd, ov);
             }
           }
       }
     };
 
-    if (team == 0) {
-#pragma unroll 1
-      for (int t = 1; t < NT; ++t) {
-        const float* sl = red + ((t - 1) * WPT + wq) * L::SLOT;
-        fold(sl[16 * NDB * 64 + lane], sl[(16 * NDB + 1) * 64 + lane],
-             [&](int j) __attribute__((always_inline)) { return sl[j * 64 + lane]; });
+    // ---- the next segment of the range: its Q and first K/V tile are loaded
+    // once this segment's results are handed off, so that their latency
+    // overlaps the hand-off (and no release waits for them)
+    const long next_u = bstart + t1;
+    const bool more = next_u < u1;
+    Seg nxt = cur;
+    if (more) nxt = decode(next_u);
+    auto prefetch = [&]() __attribute__((always_inline)) {
+      if (more) {
+        load_q(nxt, qf);  // this segment's Q fragments are no longer needed
+        gload(nxt, 0, p.k, p.k_sh, p.k_ss, goff_k, rk);
+        gload(nxt, 0, p.v, p.v_sh, p.v_ss, goff_v, rv);
       }
-    }
+    };
 
     // ---- finish the query block, or hand a partial state to the last arriver
     int nparts = 1, vf = vidx;
-    if (w.streamk) {
+    if (w.sched == kBalanced) {
       vf = range_of(bstart, w);
       nparts = range_of(bstart + nt_b - 1, w) - vf + 1;
     }
     if (nparts == 1) {
-      if (team == 0) store_out();
+      store_out();
+      prefetch();
     } else {
+      // A partial state is PART floats: one wavefront state (layout above) per
+      // wavefront; each workgroup has two slots, for the first and the last
+      // segment of its range.
+      // Byte offset of this lane's chunk k of wavefront wq's state in slot s of
+      // workgroup v (two slots: the first and the last segment of its range).
+      typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+      const __amdgpu_buffer_rsrc_t prsrc = __builtin_amdgcn_make_buffer_rsrc(w.part, (short)0, w.part_bytes, kBufferFlags);
+      auto poff = [&](int v, int s, int k) __attribute__((always_inline)) {
+        return 4 * (((v * 2 + s) * L::PART) + wq * L::SLOT + k * 256 + 4 * lane);
+      };
       const int slot = range_start(vidx, w) >= bstart ? 0 : 1;
-      float* mine = w.part + ((long)vidx * 2 + slot) * L::PART + wq * L::SLOT;
-      if (team == 0) {
+      auto pstore = [&](int k, float4 x) __attribute__((always_inline)) {
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), prsrc, poff(vidx, slot, k), 0,
+                                               kDeviceCoherent);
+      };
+      if (keeps) {
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
+        for (int j = 0; j < OWN; ++j)
 #pragma unroll
-          for (int e = 0; e < 16; ++e) mine[(db * 16 + e) * 64 + lane] = oacc[db][e];
-        mine[16 * NDB * 64 + lane] = m_run;
-        mine[(16 * NDB + 1) * 64 + lane] = l_tot;
+          for (int k = 0; k < 4; ++k)
+            pstore(4 * (own0 + j) + k, make_float4(own[j][4 * k], own[j][4 * k + 1], own[j][4 * k + 2], own[j][4 * k + 3]));
       }
-      // Release: every wavefront's stores have completed (waitcnt) before the
-      // barrier; one device-scope fence then publishes them with the arrival.
+      if (team == 0) pstore(L::NCO, make_float4(m_run, l_tot, 0.f, 0.f));
+      // Release: every wavefront's device-coherent stores have completed
+      // (vmcnt) before the barrier and so before the arrival atomic.
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
-      if (tid == 0) {
-        __threadfence();
-        arrival = atomicAdd(&w.count[hh * w.nqb + b], 1);
-      }
+      if (tid == 0) arrival = atomicAdd(&w.count[hh * w.nqb + b], 1);
+      prefetch();
       __syncthreads();
       if (arrival == nparts - 1) {  // last to arrive: merge the others and write O
-        if (tid == 0) __threadfence();  // acquire: the other parts' states are visible
-        __syncthreads();
-        if (team == 0) {
+        // The others' states were complete before their arrivals, which
+        // precede this one; device-coherent loads read them from memory.
 #pragma unroll 1
-          for (int v2 = vf; v2 < vf + nparts; ++v2) {
-            if (v2 == vidx) continue;
-            const int slot2 = range_start(v2, w) >= bstart ? 0 : 1;
-            const float* o2 = w.part + ((long)v2 * 2 + slot2) * L::PART + wq * L::SLOT;
-            // The part's weight first, then its output in 16-value batches whose
-            // loads are each issued together before being folded in.
-            const float m2 = o2[16 * NDB * 64 + lane], l2 = o2[(16 * NDB + 1) * 64 + lane];
-            const float M = fmaxf(m_run, m2);
-            const float a1 = m_run == -INFINITY ? 0.f : fast_exp2(m_run - M);
-            const float a2 = m2 == -INFINITY ? 0.f : fast_exp2(m2 - M);
-            l_tot = l_tot * a1 + l2 * a2;
-            m_run = M;
-            constexpr int HALF = 16;
-#pragma unroll
-            for (int h0 = 0; h0 < 16 * NDB; h0 += HALF) {
-              float buf[HALF];
-#pragma unroll
-              for (int j = 0; j < HALF; ++j) buf[j] = h0 + j < 16 * NDB ? o2[(h0 + j) * 64 + lane] : 0.f;
-#pragma unroll
-              for (int j = 0; j < HALF; ++j)
-                if (h0 + j < 16 * NDB) oacc[(h0 + j) / 16][(h0 + j) % 16] = fmaf(buf[j], a2, oacc[(h0 + j) / 16][(h0 + j) % 16] * a1);
-              __builtin_amdgcn_sched_barrier(0);
-            }
-          }
-          store_out();
+        for (int v2 = vf; v2 < vf + nparts; ++v2) {
+          if (v2 == vidx) continue;
+          const int slot2 = range_start(v2, w) >= bstart ? 0 : 1;
+          fold_state([&](int k) __attribute__((always_inline)) {
+            return __builtin_bit_cast(float4,
+                                      __builtin_amdgcn_raw_buffer_load_b128(prsrc, poff(v2, slot2, k), 0, kDeviceCoherent));
+          });
         }
-        if (tid == 0) w.count[hh * w.nqb + b] = 0;
+        store_out();
+        if (tid == 0) atomicExch(&w.count[hh * w.nqb + b], 0);
       }
     }
     __syncthreads();  // the LDS is restaged by the next segment
     if (!more) break;
     cur = nxt;
-    lstore(0, ka, va);
-    __syncthreads();
   }
 }
 
 // ------------------------------------------------------------------ host --
 
-static int cu_count() {
+namespace {
+
+int cu_count() {
   int dev = 0, n = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 256;
   if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
   return n;
 }
 
-// Schedule choice by a cost model in units of one unit's steady-state time
-// (about 0.66 us on MI355X), fitted to measured launches of both schedules:
-//   one workgroup per block: 10.6 + max(heaviest block, units / CUs)
-//   balanced:                45.5 + 1.44 * units per workgroup
-// The balanced schedule pays for its partial states, hand-offs and shorter
-// pipelines, so it wins only where whole blocks leave CUs idle or unevenly
-// loaded (few heads, or long blocks next to short ones).
-constexpr float kPerBlockFixed = 10.6f, kBalancedFixed = 45.5f, kBalancedPerUnit = 1.44f;
+// A launch configuration: queries per block (64: 2 wavefronts x 4 teams;
+// 128: 4 wavefronts x 2 teams) and a schedule.
+struct Config {
+  int qb;
+  int sched;
+};
 
-static Work plan(int H, int S) {
+Work plan(int H, int S, Config cfg) {
   Work w{};
-  w.nqb = (S + QB - 1) / QB;
+  w.tpb = cfg.qb / BN;
+  w.nqb = (S + cfg.qb - 1) / cfg.qb;
   w.last_nt = (S - 1) / BN + 1;
-  w.units_head = 2L * (w.nqb - 1) * w.nqb + w.last_nt;
+  w.units_head = (long)w.tpb * (w.nqb - 1) * w.nqb / 2 + w.last_nt;
   w.units = (long)H * w.units_head;
-  const int cus = cu_count();
-  // One workgroup per CU, but no range shorter than kMinUnits: a short range
-  // spends most of its time filling the pipeline, and splits a query block
-  // into many parts for its last workgroup to merge.
-  const long by_size = (w.units + kMinUnits - 1) / kMinUnits;
-  w.grid = (int)(by_size < cus ? by_size : cus);
-  const float per_cu = (float)w.units / (float)cus;
-  const float per_block = kPerBlockFixed + fmaxf((float)w.last_nt, per_cu);
-  const float balanced = kBalancedFixed + kBalancedPerUnit * (float)w.units / (float)w.grid;
-  w.streamk = balanced < per_block;
-  // NKL_FLASH_SCHEDULE=balanced|block overrides the choice (tests, tuning).
-  if (const char* force = getenv("NKL_FLASH_SCHEDULE")) {
-    if (!strcmp(force, "balanced")) w.streamk = 1;
-    if (!strcmp(force, "block")) w.streamk = 0;
+  w.sched = cfg.sched;
+  w.paired = cfg.sched != kBlock;
+  if (cfg.sched == kBalanced) {
+    // At most one workgroup per CU, and no range shorter than kMinUnits: a
+    // short range spends most of its time filling the pipeline, and splits a
+    // block into many parts for its last workgroup to merge.
+    const long by_size = (w.units + kMinUnits - 1) / kMinUnits;
+    const int cus = cu_count();
+    w.grid = (int)(by_size < cus ? by_size : cus);
+  } else if (cfg.sched == kPairs) {
+    w.grid = H * ((w.nqb + 1) / 2);
+  } else {
+    w.grid = H * w.nqb;
   }
   return w;
 }
 
-template <int D>
-static size_t part_floats() { return Layout<D>::PART; }
-
-static size_t part_floats_for(int d) {
-  return d <= 32 ? part_floats<32>() : d <= 64 ? part_floats<64>() : part_floats<128>();
+// Schedule choice, from measured launches on MI355X.  With fewer than ~12
+// units of 128-query blocks per CU, 64-query blocks halve the unit and keep
+// every CU busy; up to ~1000 units per CU the balanced schedule wins (whole
+// blocks leave CUs idle or unevenly loaded); beyond that one workgroup per
+// pair of blocks balances as well and needs no partial states.
+// NKL_FLASH_SCHEDULE=block|pairs|balanced and NKL_FLASH_QB=64|128 override
+// the choice (tests, tuning).
+Config choose(int H, int S) {
+  const long cus = cu_count();
+  const long nqb = (S + 127) / 128;
+  const long units128 = (long)H * (2 * (nqb - 1) * nqb + (S - 1) / BN + 1);
+  Config cfg = units128 < 12 * cus ? Config{64, kBalanced}
+               : units128 < 1024 * cus ? Config{128, kBalanced}
+                                       : Config{128, kPairs};
+  if (const char* f = getenv("NKL_FLASH_SCHEDULE")) {
+    if (!strcmp(f, "block")) cfg.sched = kBlock;
+    if (!strcmp(f, "pairs")) cfg.sched = kPairs;
+    if (!strcmp(f, "balanced")) cfg.sched = kBalanced;
+  }
+  if (const char* f = getenv("NKL_FLASH_QB")) {
+    if (!strcmp(f, "64")) cfg.qb = 64;
+    if (!strcmp(f, "128")) cfg.qb = 128;
+  }
+  return cfg;
 }
+
+template <int D>
+size_t part_floats(int qb) {
+  return qb == 64 ? Layout<D, 2, 4>::PART : Layout<D, 4, 2>::PART;
+}
+
+size_t part_floats_for(int d, int qb) {
+  return d <= 32 ? part_floats<32>(qb) : d <= 64 ? part_floats<64>(qb) : part_floats<128>(qb);
+}
+
+template <int D, int WPT, int NT>
+void launch(const AttnArgs& a, const Work& w, hipStream_t st) {
+  flash_bf16_kernel<D, WPT, NT><<<dim3((unsigned)w.grid), dim3(64 * WPT * NT), 0, st>>>(a, w);
+}
+
+template <int D>
+void launch_qb(const AttnArgs& a, const Work& w, int qb, hipStream_t st) {
+  if (qb == 64)
+    launch<D, 2, 4>(a, w, st);
+  else
+    launch<D, 4, 2>(a, w, st);
+}
+
+}  // namespace
 
 size_t flash_bf16_workspace_bytes(int H, int S, int d) {
   if (H <= 0 || S <= 0) return 0;
-  const Work w = plan(H, S);
-  return w.streamk ? (size_t)w.grid * 2 * part_floats_for(d) * 4 : 0;
+  const Config cfg = choose(H, S);
+  if (cfg.sched != kBalanced) return 0;
+  return (size_t)plan(H, S, cfg).grid * 2 * part_floats_for(d, cfg.qb) * 4;
 }
 
 size_t flash_bf16_counter_bytes(int H, int S) {
   if (H <= 0 || S <= 0) return 0;
-  const Work w = plan(H, S);
-  return w.streamk ? (size_t)H * w.nqb * 4 : 0;
-}
-
-template <int D>
-static void launch(const AttnArgs& a, Work w, hipStream_t st) {
-  const unsigned grid = w.streamk ? (unsigned)w.grid : (unsigned)(w.nqb * a.H);
-  flash_bf16_kernel<D><<<dim3(grid), dim3(512), 0, st>>>(a, w);
+  const Config cfg = choose(H, S);
+  if (cfg.sched != kBalanced) return 0;
+  return (size_t)H * plan(H, S, cfg).nqb * 4;
 }
 
 int flash_bf16_launch(const AttnArgs& a, void* workspace, size_t workspace_bytes, int* counters,
                       size_t counter_bytes, hipStream_t st) {
-  Work w = plan(a.H, a.S);
-  if (!workspace) {
-    w.streamk = 0;
-  } else if (w.streamk) {
+  Config cfg = choose(a.H, a.S);
+  if (cfg.sched == kBalanced && !workspace) cfg.sched = kPairs;  // the plain entry point: no scratch
+  Work w = plan(a.H, a.S, cfg);
+  if (cfg.sched == kBalanced) {
     const size_t need = flash_bf16_workspace_bytes(a.H, a.S, a.d);
     const size_t need_c = flash_bf16_counter_bytes(a.H, a.S);
     if (workspace_bytes < need || !counters || counter_bytes < need_c)
@@ -535,14 +644,15 @@ int flash_bf16_launch(const AttnArgs& a, void* workspace, size_t workspace_bytes
                        "nkl_flash_attn_causal_ws: workspace of %zu bytes and counters of %zu bytes needed, "
                        "%zu and %zu given", need, need_c, workspace_bytes, counter_bytes);
     w.part = static_cast<float*>(workspace);
+    w.part_bytes = (int)need;
     w.count = counters;
   }
   if (a.d <= 32)
-    launch<32>(a, w, st);
+    launch_qb<32>(a, w, cfg.qb, st);
   else if (a.d <= 64)
-    launch<64>(a, w, st);
+    launch_qb<64>(a, w, cfg.qb, st);
   else
-    launch<128>(a, w, st);
+    launch_qb<128>(a, w, cfg.qb, st);
   return check_launch("nkl_flash_attn_causal");
 }
 

@@ -114,15 +114,20 @@ def test_flash_scratch_reused_across_shapes(rng):
         assert rel_err(out, ref) < 1e-2, (H, S, d)
 
 
-@pytest.mark.parametrize("schedule", ["balanced", "block"])
+SCHEDULES = [(qb, s) for qb in ("64", "128") for s in ("balanced", "pairs", "block")]
+
+
+@pytest.mark.parametrize("qb,schedule", SCHEDULES)
 @pytest.mark.parametrize("H,S,d", [(1, 1, 64), (2, 65, 32), (3, 77, 128), (1, 300, 128), (4, 1000, 64),
-                                   (2, 1537, 128), (5, 640, 96), (1, 129, 128)])
-def test_flash_bf16_schedules(rng, monkeypatch, schedule, H, S, d):
-    """Both work schedules of the bf16 kernel (split query blocks merged by the
-    last workgroup, or one workgroup per block) on ragged S and several head dims."""
+                                   (2, 1537, 128), (5, 640, 96), (1, 129, 128), (1, 192, 128)])
+def test_flash_bf16_schedules(rng, monkeypatch, qb, schedule, H, S, d):
+    """Every configuration of the bf16 kernel -- 64- or 128-query blocks; split
+    blocks merged by the last workgroup, one workgroup per pair of blocks, or
+    one per block -- on ragged S and several head dims."""
     from nkilab import ops
 
     monkeypatch.setenv("NKL_FLASH_SCHEDULE", schedule)
+    monkeypatch.setenv("NKL_FLASH_QB", qb)
     q, k, v = (_bf(rng.standard_normal((H, S, d))) for _ in range(3))
     out = _np(ops.attention(q, k, v))
     ref = _sdpa_cpu(*(_np(t) for t in (q, k, v)))
@@ -130,12 +135,13 @@ def test_flash_bf16_schedules(rng, monkeypatch, schedule, H, S, d):
     np.testing.assert_allclose(out[:, 0], _np(v)[:, 0], atol=1e-2)  # query 0 sees only key 0
 
 
-@pytest.mark.parametrize("schedule", ["balanced", "block"])
-def test_flash_bf16_schedules_agree_on_config(monkeypatch, schedule):
-    """8 x 2048 x 128 under each schedule: within 3e-3 of fp32 SDPA."""
+@pytest.mark.parametrize("qb,schedule", SCHEDULES)
+def test_flash_bf16_schedules_agree_on_config(monkeypatch, qb, schedule):
+    """8 x 2048 x 128 under each configuration: within 3e-3 of fp32 SDPA."""
     from nkilab import ops, workloads
 
     monkeypatch.setenv("NKL_FLASH_SCHEDULE", schedule)
+    monkeypatch.setenv("NKL_FLASH_QB", qb)
     q, k, v = (t.cuda() for t in workloads.attention_inputs())
     out = _np(ops.attention(q, k, v))
     assert rel_err(out, _sdpa_cpu(*(_np(t) for t in (q, k, v)))) <= 3e-3
