@@ -83,7 +83,13 @@ struct Layout {
   static constexpr int SLOT = 64 * 4 * (NCO + 1);          // floats of one wavefront's state
   static constexpr int PART = WPT * SLOT;                  // floats of one partial block state
   static constexpr int XBYTES = NT * WPT * SLOT * 4;       // team hand-over area (reuses the stages)
-  static constexpr int SMEM = TOTAL * 2 > XBYTES ? TOTAL : XBYTES / 2;  // bf16 elements of LDS
+  // With two teams the main loop is staggered (see the kernel) and the Q
+  // fragments are read from LDS, after the stages, instead of held in VGPRs.
+  static constexpr bool STAGGER = NT == 2;
+  static constexpr int LDQ = D + 8;                        // Q row stride (as K's)
+  static constexpr int QOFF = TOTAL;                       // Q block, [QB][LDQ]
+  static constexpr int LOOP = STAGGER ? TOTAL + QB * LDQ : TOTAL;
+  static constexpr int SMEM = LOOP * 2 > XBYTES ? LOOP : XBYTES / 2;  // bf16 elements of LDS
 };
 
 struct Work {
@@ -171,6 +177,7 @@ __global__ __launch_bounds__(64 * WPT * NT) void flash_bf16_kernel(AttnArgs p, W
   }
   // Per-lane LDS element offsets of the MFMA operands within a stage.
   const int kfrag_off = l32 * L::LDK + 8 * h32;
+  const int qfrag_off = L::QOFF + (32 * wq + l32) * L::LDQ + 8 * h32;  // this lane's Q row in LDS
   const int i16 = lane & 15, g2 = (lane >> 4) & 1;
   const int vfrag_off = L::K_ELEMS + (4 * h32 + (i16 >> 2)) * L::LDV + 16 * g2 + 4 * (i16 & 3);
 
@@ -282,6 +289,12 @@ __global__ __launch_bounds__(64 * WPT * NT) void flash_bf16_kernel(AttnArgs p, W
     const int nit = (t1 - t0 + NT - 1) / NT;
 
     lstore(0, rk, rv);
+    if constexpr (L::STAGGER) {
+      if (team == 0) {  // both teams work on the same queries: one copy
+#pragma unroll
+        for (int f = 0; f < NQF; ++f) *reinterpret_cast<bf16x8*>(smem + qfrag_off + 16 * f) = qf[f];
+      }
+    }
     __syncthreads();
     gload(cur, 1, p.k, p.k_sh, p.k_ss, goff_k, rk);
     gload(cur, 1, p.v, p.v_sh, p.v_ss, goff_v, rv);
@@ -293,68 +306,147 @@ __global__ __launch_bounds__(64 * WPT * NT) void flash_bf16_kernel(AttnArgs p, W
 #pragma unroll
       for (int e = 0; e < 16; ++e) oacc[db][e] = 0.f;
 
-    // Step `it`: tile it computes from LDS stage it & 1; tile it + 1 (in
-    // registers since the previous step) is written to the other stage; after
-    // the barrier tile it + 2 is loaded into the registers.
-#pragma unroll 1
-    for (int it = 0; it < nit; ++it) {
-      const int tj = t0 + team + NT * it;
-      const int k0 = tj * BN;
-      const bool active = tj < t1 && k0 <= qw + 31;  // inside the segment and not above the diagonal
-      const bf16* sb = team_base + (it & 1) * L::STAGE;
-      if (active) {
-        floatx16 sacc;
+    // Online softmax of one tile's scores (keys k0 ..): masks the diagonal
+    // tile, raises the running max lazily, turns S into bf16 P.
+    auto softmax = [&](int k0, floatx16& sc, bf16x8 (&pf)[2]) __attribute__((always_inline)) {
+      if (k0 + BN - 1 > qw) {  // diagonal tile: mask keys after the query
 #pragma unroll
-        for (int e = 0; e < 16; ++e) sacc[e] = 0.f;
+        for (int e = 0; e < 16; ++e)
+          if (k0 + 8 * (e >> 2) + 4 * h32 + (e & 3) > myq) sc[e] = -INFINITY;
+      }
+      float mloc = sc[0];
 #pragma unroll
-        for (int f = 0; f < NQF; ++f) sacc = MF::mma(load_frag(sb + kfrag_off + 16 * f), qf[f], sacc);
-        __builtin_amdgcn_sched_barrier(0);
-        if (k0 + BN - 1 > qw) {  // diagonal tile: mask keys after the query
+      for (int e = 1; e < 16; ++e) mloc = fmaxf(mloc, sc[e]);
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave)) * c;
+      if (__builtin_amdgcn_ballot_w64(mloc > m_run + kRescaleSlack)) {
+        const float m_new = fmaxf(m_run, mloc);
+        const float corr = fast_exp2(m_run - m_new);
+        m_run = m_new;
+        l_run *= corr;
 #pragma unroll
-          for (int i = 0; i < 16; ++i)
-            if (k0 + 8 * (i >> 2) + 4 * h32 + (i & 3) > myq) sacc[i] = -INFINITY;
-        }
-        float mloc = sacc[0];
+        for (int db = 0; db < NDB; ++db)
 #pragma unroll
-        for (int i = 1; i < 16; ++i) mloc = fmaxf(mloc, sacc[i]);
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave)) * c;
-        if (__builtin_amdgcn_ballot_w64(mloc > m_run + kRescaleSlack)) {
-          const float m_new = fmaxf(m_run, mloc);
-          const float corr = fast_exp2(m_run - m_new);
-          m_run = m_new;
-          l_run *= corr;
+          for (int e = 0; e < 16; ++e) oacc[db][e] *= corr;
+      }
+      float rs = 0.f;
 #pragma unroll
-          for (int db = 0; db < NDB; ++db)
+      for (int e = 0; e < 16; ++e) {
+        sc[e] = fast_exp2(fmaf(sc[e], c, -m_run));
+        rs += sc[e];
+      }
+      l_run += rs;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) oacc[db][e] *= corr;
-        }
-        float rs = 0.f;
+      for (int uu = 0; uu < 2; ++uu)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          sacc[i] = fast_exp2(fmaf(sacc[i], c, -m_run));
-          rs += sacc[i];
-        }
-        l_run += rs;
-        bf16x8 pf[2];
+        for (int j = 0; j < 8; ++j) pf[uu][j] = (bf16)sc[8 * uu + j];
+    };
+    // O += P V for the tile in stage sb.  The V^T fragments of two d-blocks
+    // are read together before their MFMAs, so that the MFMAs wait on LDS
+    // once per pair of d-blocks rather than once each.
+    auto pv = [&](const bf16* sb, const bf16x8 (&pf)[2]) __attribute__((always_inline)) {
+      constexpr int G = NDB >= 2 ? 2 : 1;
 #pragma unroll
-        for (int uu = 0; uu < 2; ++uu)
+      for (int d0 = 0; d0 < NDB; d0 += G) {
+        bf16x8 a[G][2];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) pf[uu][j] = (bf16)sacc[8 * uu + j];
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) {
+        for (int g = 0; g < G; ++g)
 #pragma unroll
           for (int uu = 0; uu < 2; ++uu) {
-            const bf16* vaddr = sb + vfrag_off + 16 * uu * L::LDV + 32 * db;
-            const bf16x8 a = read_vt_frag(vaddr, vaddr + 8 * L::LDV);
-            oacc[db] = MF::mma(a, pf[uu], oacc[db]);
+            const bf16* vaddr = sb + vfrag_off + 16 * uu * L::LDV + 32 * (d0 + g);
+            a[g][uu] = read_vt_frag(vaddr, vaddr + 8 * L::LDV);
+          }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+          for (int uu = 0; uu < 2; ++uu) oacc[d0 + g] = MF::mma(a[g][uu], pf[uu], oacc[d0 + g]);
+      }
+    };
+
+    if constexpr (L::STAGGER) {
+      // Two phases per tile i, each ended by a barrier:
+      //   M(i)  O += P(i-1) V(i-1), then S(i) = K(i) Q^T            (MFMA)
+      //   V(i)  softmax of S(i) into P(i); tile i+1 from registers to
+      //         LDS stage (i+1) & 1; tile i+2 loaded into the registers (VALU)
+      // Teams of the second half run one phase behind, so that on every SIMD
+      // (which holds one wavefront of each half) one wavefront is in an M phase
+      // while the other is in a V phase.  Stage (i+1) & 1 was last read in M(i),
+      // one barrier before V(i) writes it; K(i+1) written in V(i) is read in
+      // M(i+1), one barrier later.
+      // Both halves run the same straight-line body; the lagging half takes
+      // one extra barrier first, the leading half one extra at the end.
+      const bool lagged = team >= NT / 2;
+      floatx16 sacc;
+      bf16x8 pf[2];
+      bool act_prev = false;  // tile i-1 was computed (P valid)
+      if (lagged) __syncthreads();
+#pragma unroll 1
+      for (int i = 0; i < nit; ++i) {
+        // ---- M(i)
+        if (act_prev) pv(team_base + ((i - 1) & 1) * L::STAGE, pf);  // O += P(i-1) V(i-1)
+        __builtin_amdgcn_sched_barrier(0);  // V(i-1) fragments die before K(i)'s are read
+        const int tj = t0 + team + NT * i;
+        // inside the segment and not above the diagonal (uniform over the wavefront)
+        const bool act = __builtin_amdgcn_readfirstlane(tj < t1 && tj * BN <= qw + 31);
+        if (act) {  // S(i) = K(i) Q^T
+          const bf16* sb = team_base + (i & 1) * L::STAGE;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) sacc[e] = 0.f;
+          // K and Q fragments four at a time, read before their MFMAs
+          constexpr int FG = NQF >= 4 ? 4 : NQF;
+#pragma unroll
+          for (int f0 = 0; f0 < NQF; f0 += FG) {
+            bf16x8 kf[FG], qq[FG];
+#pragma unroll
+            for (int f = 0; f < FG; ++f) {
+              kf[f] = load_frag(sb + kfrag_off + 16 * (f0 + f));
+              qq[f] = load_frag(smem + qfrag_off + 16 * (f0 + f));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int f = 0; f < FG; ++f) sacc = MF::mma(kf[f], qq[f], sacc);
           }
         }
+        __syncthreads();
+        // ---- V(i)
+        if (act) softmax(tj * BN, sacc, pf);
+        act_prev = act;
+        lstore((i + 1) & 1, rk, rv);
+        gload(cur, i + 2, p.k, p.k_sh, p.k_ss, goff_k, rk);
+        gload(cur, i + 2, p.v, p.v_sh, p.v_ss, goff_v, rv);
+        __syncthreads();
       }
-      lstore((it + 1) & 1, rk, rv);
+      // ---- M(nit): the last tile's P V
+      if (act_prev) pv(team_base + ((nit - 1) & 1) * L::STAGE, pf);
       __syncthreads();
-      gload(cur, it + 2, p.k, p.k_sh, p.k_ss, goff_k, rk);
-      gload(cur, it + 2, p.v, p.v_sh, p.v_ss, goff_v, rv);
+      if (!lagged) __syncthreads();
+    } else {
+      // One step per tile: tile it computes from LDS stage it & 1; tile it + 1
+      // (in registers since the previous step) is written to the other stage;
+      // after the barrier tile it + 2 is loaded into the registers.
+#pragma unroll 1
+      for (int it = 0; it < nit; ++it) {
+        const int tj = t0 + team + NT * it;
+        const int k0 = tj * BN;
+        const bool active = tj < t1 && k0 <= qw + 31;  // inside the segment and not above the diagonal
+        const bf16* sb = team_base + (it & 1) * L::STAGE;
+        if (active) {
+          floatx16 sacc;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) sacc[e] = 0.f;
+#pragma unroll
+          for (int f = 0; f < NQF; ++f) sacc = MF::mma(load_frag(sb + kfrag_off + 16 * f), qf[f], sacc);
+          __builtin_amdgcn_sched_barrier(0);
+          bf16x8 pf[2];
+          softmax(k0, sacc, pf);
+          __builtin_amdgcn_sched_barrier(0);
+          pv(sb, pf);
+        }
+        lstore((it + 1) & 1, rk, rv);
+        __syncthreads();
+        gload(cur, it + 2, p.k, p.k_sh, p.k_ss, goff_k, rk);
+        gload(cur, it + 2, p.v, p.v_sh, p.v_ss, goff_v, rv);
+      }
     }
 
     // ---- hand-over between the teams.  Team t finishes d-blocks
