@@ -617,6 +617,453 @@ __global__ __launch_bounds__(64 * WPT * NT) void flash_bf16_kernel(AttnArgs p, W
   }
 }
 
+// ------------------------------------------------- one wavefront per SIMD --
+//
+// The same unit schedules with 128-query blocks and d in (64, 128], as one
+// team of 4 wavefronts (one per SIMD), each holding 512 registers.  The
+// wavefront overlaps its own MFMA and VALU work: the QK^T MFMAs of tile i+1
+// are issued before the softmax and P V of tile i.  K/V tiles are copied
+// global -> LDS by the buffer unit (buffer_load ... lds: lane l's 16 bytes
+// land at the instruction's LDS base + 16 l), W1_NS - 2 tiles ahead of use,
+// into W1_NS stages of unpadded 256-byte rows whose 16-byte chunks are
+// swizzled: logical chunk c of row r sits at chunk c ^ w1_swz(r), with
+// w1_swz(r) = 4 (r % 4) + 2 ((r / 4) % 2) + (r / 8) % 2.  The 16 rows of a
+// K-fragment read (b128, one chunk each, also as rows 0-7 x chunks 2f, 2f+1)
+// and the 4 aligned rows x 4 aligned chunks of a transposed V read (b64)
+// then all fall in distinct bank groups.  W1_NS = 4 stages of 16 KB keep
+// every stage-relative LDS offset an instruction immediate (the loop is
+// unrolled by the stage count).
+
+namespace {
+
+constexpr int W1_NS = 4;                    // LDS stages (offsets stay below 64 KB)
+constexpr int W1_ROWB = 256;                // bytes of a K/V row (d = 128)
+constexpr int W1_TILEB = BN * W1_ROWB;      // bytes of a K (or V) tile
+constexpr int W1_STAGEB = 2 * W1_TILEB;     // K tile then V tile
+constexpr int W1_LPT = 4;                   // DMA instructions per tile per wavefront (2 K + 2 V)
+
+__device__ __forceinline__ int w1_swz(int r) { return ((r & 3) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1); }
+
+// s_waitcnt with vmcnt <= n and the other counters left alone (gfx9 encoding).
+template <int n>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+}  // namespace
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void flash_bf16_w1_kernel(AttnArgs p, Work w) {
+  constexpr int D = 128, NQF = D / 16, NDB = D / 32, QB = 128, WPT = 4;
+  constexpr int NCO = 4 * NDB, SLOT = 64 * 4 * (NCO + 1), PART = WPT * SLOT;
+  using MF = Mfma32<bf16>;
+  __shared__ __align__(16) unsigned char lds[W1_NS * W1_STAGEB];
+  __shared__ int arrival;
+  // Declaring an AGPR use makes the compiler select the MFMA form whose
+  // accumulators live in AGPRs, which keeps O there for the whole loop.
+  asm volatile("" ::: "a255");
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wq = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h32 = lane >> 5, l32 = lane & 31;
+  const int S = p.S, dlim = p.d;
+  const float c = p.c;
+
+  // Per-lane byte offsets within a stage.
+  //   K fragment f: row l32, logical chunk 2 f + h32.
+  int koff[NQF];
+  {
+    const int sw = w1_swz(l32);
+#pragma unroll
+    for (int f = 0; f < NQF; ++f) koff[f] = l32 * W1_ROWB + (((2 * f + h32) ^ sw) << 4);
+  }
+  //   V^T fragment (d-block db, first or second 8-row read): rows
+  //   r0 + 8 half (+ 16 uu, a constant 4096 bytes), d = 32 db + 16 g2 + 4 (i16 % 4).
+  int voff[NDB][2];
+  {
+    const int i16 = lane & 15, g2 = (lane >> 4) & 1;
+    const int r0 = 4 * h32 + (i16 >> 2);
+    const int cb = 2 * g2 + ((i16 & 3) >> 1);
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int row = r0 + 8 * half;
+        voff[db][half] = W1_TILEB + row * W1_ROWB + (((4 * db + cb) ^ w1_swz(row)) << 4) + (i16 & 1) * 8;
+      }
+  }
+  //   DMA: this wavefront copies rows 8 wq .. 8 wq + 7 of each tile, as two
+  //   1 KB instructions n = 2 wq + u (rows 4 n .. 4 n + 3); lane l fills
+  //   row 4 n + l / 16, physical chunk l % 16.  Chunks past d read as zero.
+  int dk[2], dv[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int row = 4 * (2 * wq + u) + (lane >> 4);
+    const int lc = (lane & 15) ^ w1_swz(row);
+    const bool ok = lc * 8 < dlim;
+    dk[u] = ok ? 2 * (row * (int)p.k_ss + lc * 8) : 0x40000000;
+    dv[u] = ok ? 2 * (row * (int)p.v_ss + lc * 8) : 0x40000000;
+  }
+
+  // This workgroup's unit range [u0, u1).
+  long u0, u1;
+  int vidx = blockIdx.x;
+  if (w.sched == kBalanced) {
+    if (w.grid % 8 == 0) vidx = (blockIdx.x % 8) * (w.grid / 8) + blockIdx.x / 8;
+    u0 = range_start(vidx, w);
+    u1 = range_start(vidx + 1, w);
+  } else if (w.sched == kPairs) {
+    const int hh = blockIdx.x % p.H, k = blockIdx.x / p.H;
+    u0 = hh * w.units_head + pair_before(k, w);
+    u1 = 2 * k + 2 <= w.nqb ? hh * w.units_head + pair_before(k + 1, w) : (hh + 1) * w.units_head;
+  } else {
+    const int hh = blockIdx.x % p.H;
+    const int b = w.nqb - 1 - blockIdx.x / p.H;
+    u0 = hh * w.units_head + plain_before(b, w);
+    u1 = u0 + block_tiles(b, w);
+  }
+
+  struct Seg {
+    int hh, b, t0, t1, nt;
+    long bstart;
+  };
+  auto decode = [&](long u) __attribute__((always_inline)) {
+    Seg sg;
+    sg.hh = (int)(u / w.units_head);
+    const long r = u - (long)sg.hh * w.units_head;
+    long before;
+    if (w.paired) {
+      const long full = (long)w.tpb * (w.nqb + 1);
+      const long delta = (long)w.tpb * w.nqb - w.last_nt;
+      const int k = min((int)((r + delta) / full), (w.nqb - 1) / 2);
+      before = pair_before(k, w);
+      const int na = block_tiles(k, w);
+      if (r - before < na) {
+        sg.b = k;
+      } else {
+        sg.b = w.nqb - 1 - k;
+        before += na;
+      }
+    } else {
+      int b = (int)((sqrtf(1.0f + 8.0f * (float)r / (float)w.tpb) - 1.0f) * 0.5f);
+      b = max(0, min(b, w.nqb - 1));
+      while (b + 1 <= w.nqb - 1 && plain_before(b + 1, w) <= r) ++b;
+      while (b > 0 && plain_before(b, w) > r) --b;
+      sg.b = b;
+      before = plain_before(b, w);
+    }
+    sg.bstart = (long)sg.hh * w.units_head + before;
+    sg.nt = block_tiles(sg.b, w);
+    sg.t0 = (int)(u - sg.bstart);
+    sg.t1 = (int)(min(u1, sg.bstart + sg.nt) - sg.bstart);
+    return sg;
+  };
+  bf16x8 qf[NQF];
+  auto load_q = [&](const Seg& sg) __attribute__((always_inline)) {
+    const bf16* Q = static_cast<const bf16*>(p.q) + (long)sg.hh * p.q_sh;
+    const int qrow = QB * sg.b + 32 * wq + l32;
+#pragma unroll
+    for (int f = 0; f < NQF; ++f) {
+      const int dd = 16 * f + 8 * h32;
+      qf[f] = __builtin_bit_cast(bf16x8, ld16_or_zero(Q, (long)qrow * p.q_ss + dd, qrow < S && dd < dlim));
+    }
+  };
+  // Copies tile j (0-based within the segment) of K and V into LDS stage st;
+  // tiles past the segment copy zeros (no memory is read).
+  auto dma = [&](const Seg& sg, int j, int st) __attribute__((always_inline)) {
+    const int tj = sg.t0 + j;
+    const int k0 = tj * BN;
+    const int nkeys = tj < sg.t1 ? min(BN, S - k0) : 0;
+    const int kbytes = nkeys > 0 ? 2 * ((nkeys - 1) * (int)p.k_ss + dlim) : 0;
+    const int vbytes = nkeys > 0 ? 2 * ((nkeys - 1) * (int)p.v_ss + dlim) : 0;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(static_cast<const bf16*>(p.k) + (long)sg.hh * p.k_sh + (long)k0 * p.k_ss), (short)0, kbytes,
+        kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(static_cast<const bf16*>(p.v) + (long)sg.hh * p.v_sh + (long)k0 * p.v_ss), (short)0, vbytes,
+        kBufferFlags);
+    unsigned char* sb = lds + st * W1_STAGEB;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int n = 2 * wq + u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(sb + n * 1024), 16,
+                                               dk[u], 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(sb + W1_TILEB + n * 1024),
+                                               16, dv[u], 0, 0, 0);
+    }
+  };
+
+  Seg cur = decode(u0);
+  load_q(cur);
+
+  for (;;) {
+    const int hh = cur.hh, b = cur.b, t0 = cur.t0, t1 = cur.t1, nt_b = cur.nt;
+    const long bstart = cur.bstart;
+    const int qw = QB * b + 32 * wq;
+    const int myq = qw + l32;
+    const int nt = t1 - t0;
+
+#pragma unroll
+    for (int j = 0; j < W1_NS - 1; ++j) dma(cur, j, j);
+    wait_vm<(W1_NS - 2) * W1_LPT>();  // tile 0 has landed (and Q)
+    __syncthreads();
+
+    float m_run = -INFINITY, l_run = 0.f;
+    floatx16 oacc[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) oacc[db][e] = 0.f;
+
+    // Software pipeline, per tile i (two scheduling regions, each a
+    // fixed interleave of MFMA and VALU instructions):
+    //   region 1: S(i+1) = K(i+1) Q^T     x  exp, row sums, bf16 P(i)
+    //   region 2: O += P(i) V(i)          x  mask and row max of S(i+1)
+    //   then the lazy rescale decision for tile i+1.
+    // Every tile runs the same instructions: keys past a query or past the
+    // segment are masked to -inf, so a tile wholly above a wavefront's
+    // diagonal contributes exact zeros.
+    const int klim_seg = (t0 + nt) * BN;  // keys at or past this are outside the segment
+    auto mask_max = [&](int j, floatx16& sc) __attribute__((always_inline)) {
+      const int k0 = (t0 + j) * BN;
+      const int lim = min(myq, klim_seg - 1);  // last key this query may see in the segment
+      float mx = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        sc[e] = k0 + 8 * (e >> 2) + 4 * h32 + (e & 3) > lim ? -INFINITY : sc[e];
+        mx = fmaxf(mx, sc[e]);
+      }
+      return mx;
+    };
+    auto plain_max = [&](const floatx16& sc) __attribute__((always_inline)) {
+      float mx = sc[0];
+#pragma unroll
+      for (int e = 1; e < 16; ++e) mx = fmaxf(mx, sc[e]);
+      return mx;
+    };
+    // Tile j needs masking when it reaches past this wavefront's first query
+    // or lies outside the segment (uniform over the wavefront).
+    auto needs_mask = [&](int j) __attribute__((always_inline)) {
+      return (bool)__builtin_amdgcn_readfirstlane(j >= nt || (t0 + j) * BN + BN - 1 > qw);
+    };
+    // Raises the running max when the tile's max exceeds it by the slack
+    // (rescaling O and l after the P V of the previous tile).
+    auto rescale = [&](float mx) __attribute__((always_inline)) {
+      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave)) * c;
+      if (__builtin_amdgcn_ballot_w64(mx > m_run + kRescaleSlack)) {
+        const float m_new = fmaxf(m_run, mx);
+        const float corr = m_run == -INFINITY ? 0.f : fast_exp2(m_run - m_new);
+        m_run = m_new;
+        l_run *= corr;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) oacc[db][e] *= corr;
+      }
+    };
+    auto kfrags = [&](int st, bf16x8 (&kf)[NQF]) __attribute__((always_inline)) {
+      const unsigned char* sb = lds + st * W1_STAGEB;
+#pragma unroll
+      for (int f = 0; f < NQF; ++f) kf[f] = *reinterpret_cast<const bf16x8*>(sb + koff[f]);
+    };
+    auto vfrags = [&](int st, bf16x8 (&a)[NDB][2]) __attribute__((always_inline)) {
+      typedef short shortx4 __attribute__((ext_vector_type(4)));
+      typedef __attribute__((address_space(3))) shortx4 lds_s4;
+      const unsigned char* sb = lds + st * W1_STAGEB;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int uu = 0; uu < 2; ++uu) {
+          const shortx4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(sb + voff[db][0] + 4096 * uu));
+          const shortx4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(sb + voff[db][1] + 4096 * uu));
+          a[db][uu] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+    };
+
+    floatx16 s0, s1;
+    {  // S(0), its mask, max and rescale
+      bf16x8 kf[NQF];
+      kfrags(0, kf);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s0[e] = 0.f;
+#pragma unroll
+      for (int f = 0; f < NQF; ++f) s0 = MF::mma(kf[f], qf[f], s0);
+      rescale(needs_mask(0) ? mask_max(0, s0) : plain_max(s0));
+    }
+    auto step = [&](int i, int st, floatx16& sc, floatx16& sn) __attribute__((always_inline)) {
+      const int st1 = (st + 1) % W1_NS, stp = (st + W1_NS - 1) % W1_NS;
+      wait_vm<(W1_NS - 3) * W1_LPT>();  // tile i+1 has landed
+      __syncthreads();                  // ... for every wavefront; all are done with tile i-1
+      dma(cur, i + W1_NS - 1, stp);     // into tile i-1's stage
+      bf16x8 kf[NQF], va[NDB][2];
+      kfrags(st1, kf);  // every fragment read of the tile is in flight
+      vfrags(st, va);   // before the first MFMA waits for one
+      const bool msk = needs_mask(i + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      // ---- region 1: S(i+1) MFMAs x exp / sums / P(i)
+      const float mneg = m_run == -INFINITY ? 0.f : -m_run;  // an empty row keeps exp2(-inf) = 0
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sn[e] = 0.f;
+      float rs = 0.f;
+      bf16x8 pf[2];
+#pragma unroll
+      for (int f = 0; f < NQF; ++f) {
+        sn = MF::mma(kf[f], qf[f], sn);
+#pragma unroll
+        for (int e = 2 * f; e < 2 * f + 2; ++e) {
+          sc[e] = fast_exp2(fmaf(sc[e], c, mneg));
+          rs += sc[e];
+        }
+      }
+#pragma unroll
+      for (int uu = 0; uu < 2; ++uu)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pf[uu][j] = (bf16)sc[8 * uu + j];
+      l_run += rs;
+#pragma unroll
+      for (int f = 0; f < NQF; ++f) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // six VALU
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // ---- region 2: O += P(i) V(i) x (mask and) max of S(i+1)
+      float mx;
+      if (msk) {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int uu = 0; uu < 2; ++uu) oacc[db] = MF::mma(va[db][uu], pf[uu], oacc[db]);
+        mx = mask_max(i + 1, sn);
+#pragma unroll
+        for (int k = 0; k < 2 * NDB; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+          __builtin_amdgcn_sched_group_barrier(0x002, 5, 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      } else {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int uu = 0; uu < 2; ++uu) oacc[db] = MF::mma(va[db][uu], pf[uu], oacc[db]);
+        mx = plain_max(sn);
+#pragma unroll
+        for (int k = 0; k < 2 * NDB; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 2);
+          __builtin_amdgcn_sched_group_barrier(0x002, 2, 2);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      rescale(mx);
+    };
+    static_assert(W1_NS == 4, "the loop below is unrolled by the stage count");
+#pragma unroll 1
+    for (int i = 0; i < nt; i += 4) {
+      step(i, 0, s0, s1);
+      if (i + 1 >= nt) break;
+      step(i + 1, 1, s1, s0);
+      if (i + 2 >= nt) break;
+      step(i + 2, 2, s0, s1);
+      if (i + 3 >= nt) break;
+      step(i + 3, 3, s1, s0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the copies of tiles past the segment have landed
+    __syncthreads();
+
+    float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
+    auto weights = [&](float m2, float l2, float& a1, float& a2) __attribute__((always_inline)) {
+      const float M = fmaxf(m_run, m2);
+      a1 = m_run == -INFINITY ? 0.f : fast_exp2(m_run - M);
+      a2 = m2 == -INFINITY ? 0.f : fast_exp2(m2 - M);
+      l_tot = l_tot * a1 + l2 * a2;
+      m_run = M;
+    };
+    auto store_out = [&]() __attribute__((always_inline)) {
+      const float linv = 1.0f / l_tot;
+      if (myq < S) {
+        bf16* orow = static_cast<bf16*>(p.o) + (long)hh * p.o_sh + (long)myq * p.o_ss;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int bq = 0; bq < 4; ++bq) {
+            const int dd = 32 * db + 8 * bq + 4 * h32;
+            if (dd < dlim) {
+              float ov[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) ov[e] = oacc[db][4 * bq + e] * linv;
+              store_vec<4>(orow + dd, ov);
+            }
+          }
+      }
+    };
+
+    const long next_u = bstart + t1;
+    const bool more = next_u < u1;
+    Seg nxt = cur;
+    if (more) nxt = decode(next_u);
+
+    int nparts = 1, vf = vidx;
+    if (w.sched == kBalanced) {
+      vf = range_of(bstart, w);
+      nparts = range_of(bstart + nt_b - 1, w) - vf + 1;
+    }
+    if (nparts == 1) {
+      store_out();
+      if (more) load_q(nxt);
+    } else {
+      typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+      const __amdgpu_buffer_rsrc_t prsrc = __builtin_amdgcn_make_buffer_rsrc(w.part, (short)0, w.part_bytes, kBufferFlags);
+      auto poff = [&](int v, int s2, int k) __attribute__((always_inline)) {
+        return 4 * (((v * 2 + s2) * PART) + wq * SLOT + k * 256 + 4 * lane);
+      };
+      const int slot = range_start(vidx, w) >= bstart ? 0 : 1;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          __builtin_amdgcn_raw_buffer_store_b128(
+              __builtin_bit_cast(u32x4, make_float4(oacc[db][4 * k], oacc[db][4 * k + 1], oacc[db][4 * k + 2],
+                                                    oacc[db][4 * k + 3])),
+              prsrc, poff(vidx, slot, 4 * db + k), 0, kDeviceCoherent);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, make_float4(m_run, l_tot, 0.f, 0.f)), prsrc,
+                                             poff(vidx, slot, NCO), 0, kDeviceCoherent);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (tid == 0) arrival = atomicAdd(&w.count[hh * w.nqb + b], 1);
+      if (more) load_q(nxt);
+      __syncthreads();
+      if (arrival == nparts - 1) {
+#pragma unroll 1
+        for (int v2 = vf; v2 < vf + nparts; ++v2) {
+          if (v2 == vidx) continue;
+          const int slot2 = range_start(v2, w) >= bstart ? 0 : 1;
+          float4 v[NCO + 1];
+#pragma unroll
+          for (int k = 0; k <= NCO; ++k)
+            v[k] = __builtin_bit_cast(float4,
+                                      __builtin_amdgcn_raw_buffer_load_b128(prsrc, poff(v2, slot2, k), 0, kDeviceCoherent));
+          float a1, a2;
+          weights(v[NCO].x, v[NCO].y, a1, a2);
+#pragma unroll
+          for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              oacc[db][4 * k] = fmaf(v[4 * db + k].x, a2, oacc[db][4 * k] * a1);
+              oacc[db][4 * k + 1] = fmaf(v[4 * db + k].y, a2, oacc[db][4 * k + 1] * a1);
+              oacc[db][4 * k + 2] = fmaf(v[4 * db + k].z, a2, oacc[db][4 * k + 2] * a1);
+              oacc[db][4 * k + 3] = fmaf(v[4 * db + k].w, a2, oacc[db][4 * k + 3] * a1);
+            }
+        }
+        store_out();
+        if (tid == 0) atomicExch(&w.count[hh * w.nqb + b], 0);
+      }
+    }
+    __syncthreads();
+    if (!more) break;
+    cur = nxt;
+  }
+}
+
 // ------------------------------------------------------------------ host --
 
 namespace {
@@ -738,6 +1185,14 @@ int flash_bf16_launch(const AttnArgs& a, void* workspace, size_t workspace_bytes
     w.part = static_cast<float*>(workspace);
     w.part_bytes = (int)need;
     w.count = counters;
+  }
+  // The one-wavefront-per-SIMD kernel takes 128-query blocks with
+  // 64 < d <= 128; NKL_FLASH_KERNEL=w1|teams overrides.
+  bool w1 = false;
+  if (const char* f = getenv("NKL_FLASH_KERNEL")) w1 = !strcmp(f, "w1");
+  if (w1 && cfg.qb == 128 && a.d > 64) {
+    flash_bf16_w1_kernel<<<dim3((unsigned)w.grid), dim3(256), 0, st>>>(a, w);
+    return check_launch("nkl_flash_attn_causal");
   }
   if (a.d <= 32)
     launch_qb<32>(a, w, cfg.qb, st);
