@@ -14,6 +14,8 @@
 // kernel's 16-byte loads cannot address): each wavefront computes one 32x32
 // tile of C reading its operands straight from global memory at every K step
 // -- no on-chip reuse, like the reference's matmul_naive.
+#include <type_traits>
+
 #include "common.h"
 
 namespace nkl {
@@ -239,6 +241,225 @@ __global__ __launch_bounds__(256) void gemm_naive_kernel(GemmArgs p) {
   }
 }
 
+// ------------------------------------------------ bf16 GEMM, LDS-DMA staged --
+//
+// The bf16 path.  Operand tiles are copied global -> LDS by the buffer unit
+// (buffer_load ... lds, lane l's 16 bytes at the instruction's LDS base + 16 l)
+// into a ring of NS stages, NS - 1 K-steps ahead of use, so that even a small
+// GEMM (1024^3, 256 workgroups of 64x64) keeps enough loads in flight to cover
+// the memory latency.  Every staged tile is made of 128-byte rows (64 bf16 of
+// K for A and for B given as [N, K]; 64 columns of N for B given as [K, N],
+// in sub-tiles of 64 columns) whose 16-byte chunks are swizzled: chunk c of
+// row r sits at chunk c ^ g_swz(r).  The swizzle keeps the 16-row b128
+// fragment reads (A, B^T) and the 4-row transposed b64 reads (B as [K, N],
+// read with ds_read_b64_tr_b16) free of bank conflicts.  One barrier per
+// K-step; 2x2 wavefronts of 32x32x16 MFMA tiles.
+
+namespace {
+
+constexpr int G_BK = 64;  // K elements per stage
+
+__device__ __forceinline__ int g_swz(int r) { return (((r >> 1) & 1) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1); }
+// Byte offset of 16-byte chunk c of row r in a tile of 128-byte rows.
+__device__ __forceinline__ int g_pos(int r, int c) { return r * 128 + ((c ^ g_swz(r)) << 4); }
+
+template <int n>
+__device__ __forceinline__ void g_wait_vm() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+constexpr unsigned kOOB = 0x80000000u;  // a buffer offset past every range: the lane reads zeros
+
+}  // namespace
+
+template <typename TO, int BM, int BN, bool BT, int NS>
+__global__ __launch_bounds__(256) void gemm_dma_kernel(GemmArgs p) {
+  using MF = Mfma32<bf16>;
+  constexpr int A_BYTES = BM * 128;
+  constexpr int B_BYTES = BN * 128;  // BN rows of 128 B (B^T) or BN / 64 sub-tiles of 64 x 128 B
+  constexpr int STAGE = A_BYTES + B_BYTES;
+  constexpr int A_PW = A_BYTES / 1024 / 4, B_PW = B_BYTES / 1024 / 4;  // DMA instructions per wavefront
+  constexpr int LPT = A_PW + B_PW;
+  constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
+  static_assert(A_PW >= 1 && B_PW >= 1, "tile too small");
+  static_assert((NS - 2) * LPT < 64, "vmcnt range");
+  __shared__ __align__(16) unsigned char lds[NS * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wid >> 1, wn = wid & 1;
+  const int tiles_m = (p.M + BM - 1) / BM, tiles_n = (p.N + BN - 1) / BN;
+  int tm, tn;
+  tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int bz = blockIdx.z;
+  const bf16* A = static_cast<const bf16*>(p.A) + (long)bz * p.sA;
+  const bf16* B = static_cast<const bf16*>(p.B) + (long)bz * p.sB;
+  TO* C = static_cast<TO*>(p.C) + (long)bz * p.sC;
+  const TO* R = p.R ? static_cast<const TO*>(p.R) + (long)bz * p.sR : nullptr;
+  const int K = p.K;
+
+  // ---- DMA: instruction q of a 128-byte-row tile covers rows 8 q .. 8 q + 7;
+  // lane l fills row 8 q + l / 8, physical chunk l % 8.
+  const int dr = lane >> 3, dpc = lane & 7;
+  // A rows m (B^T rows n): byte offset of the lane's chunk at K-step 0, or kOOB.
+  const int rows_a = min(BM, p.M - m0);
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(A + (long)m0 * p.lda), (short)0, (int)min(2L * ((rows_a - 1) * p.lda + K), 0x7fffffffL), 0x00020000);
+  unsigned aoff[A_PW];
+  int akc[A_PW];
+#pragma unroll
+  for (int u = 0; u < A_PW; ++u) {
+    const int row = 8 * (wid * A_PW + u) + dr;
+    const int lc = dpc ^ g_swz(row);
+    akc[u] = 8 * lc;
+    aoff[u] = row < rows_a ? (unsigned)(2 * ((long)row * p.lda + 8 * lc)) : kOOB;
+  }
+  __amdgpu_buffer_rsrc_t rb;
+  unsigned boff[B_PW];
+  int bkc[B_PW], brow[B_PW];
+  if constexpr (BT) {
+    const int rows_b = min(BN, p.N - n0);
+    rb = __builtin_amdgcn_make_buffer_rsrc((void*)(B + (long)n0 * p.ldb), (short)0,
+                                           (int)min(2L * ((rows_b - 1) * p.ldb + K), 0x7fffffffL), 0x00020000);
+#pragma unroll
+    for (int u = 0; u < B_PW; ++u) {
+      const int row = 8 * (wid * B_PW + u) + dr;
+      const int lc = dpc ^ g_swz(row);
+      bkc[u] = 8 * lc;
+      brow[u] = 0;
+      boff[u] = row < rows_b ? (unsigned)(2 * ((long)row * p.ldb + 8 * lc)) : kOOB;
+    }
+  } else {
+    // [K, N]: instruction q -> sub-tile q / 8 (64 columns), k rows 8 (q % 8) + dr.
+    const int cols_b = min(BN, p.N - n0);
+    rb = __builtin_amdgcn_make_buffer_rsrc((void*)(B + n0), (short)0,
+                                           (int)min(2L * ((long)(K - 1) * p.ldb + cols_b), 0x7fffffffL), 0x00020000);
+#pragma unroll
+    for (int u = 0; u < B_PW; ++u) {
+      const int q = wid * B_PW + u;
+      const int sub = q / 8, row = 8 * (q % 8) + dr;
+      const int col = 64 * sub + 8 * (dpc ^ g_swz(row));
+      brow[u] = row;
+      bkc[u] = 0;
+      boff[u] = col < cols_b ? (unsigned)(2 * ((long)row * p.ldb + col)) : kOOB;
+    }
+  }
+  // Copies K-step s into stage st (K-steps past K copy zeros).
+  auto dma = [&](int s, int st) __attribute__((always_inline)) {
+    const int k0 = s * G_BK;
+    unsigned char* sb = lds + st * STAGE;
+#pragma unroll
+    for (int u = 0; u < A_PW; ++u) {
+      const unsigned off = (aoff[u] != kOOB && k0 + akc[u] < K) ? aoff[u] + 2u * k0 : kOOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (__attribute__((address_space(3))) void*)(sb + (wid * A_PW + u) * 1024),
+                                               16, (int)off, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < B_PW; ++u) {
+      unsigned off;
+      if constexpr (BT)
+        off = (boff[u] != kOOB && k0 + bkc[u] < K) ? boff[u] + 2u * k0 : kOOB;
+      else
+        off = (boff[u] != kOOB && k0 + brow[u] < K) ? boff[u] + (unsigned)(2L * k0 * p.ldb) : kOOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rb, (__attribute__((address_space(3))) void*)(sb + A_BYTES + (wid * B_PW + u) * 1024), 16, (int)off, 0, 0,
+          0);
+    }
+  };
+
+  // ---- fragment offsets within a stage (K-step sub-step ks = 0..3)
+  const int lr = lane & 31, lg = lane >> 5;
+  int afo[TM][4], bfo[TN][4][2];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) afo[i][ks] = g_pos(wm * WM + i * 32 + lr, 2 * ks + lg);
+  {
+    const int i16 = lane & 15, g2 = (lane >> 4) & 1;
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        if constexpr (BT) {
+          bfo[j][ks][0] = A_BYTES + g_pos(wn * WN + j * 32 + lr, 2 * ks + lg);
+          bfo[j][ks][1] = 0;
+        } else {
+          // lane i of a 16-lane group reads row k (4 per read) at columns n .. n + 3
+          const int n = wn * WN + j * 32 + 16 * g2 + 4 * (i16 & 3);
+          const int sub = n / 64, nc = n % 64;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int krow = 16 * ks + 8 * lg + 4 * h + (i16 >> 2);
+            bfo[j][ks][h] = A_BYTES + sub * 8192 + g_pos(krow, nc / 8) + (nc % 8) * 2;
+          }
+        }
+      }
+  }
+
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  const int nk = (K + G_BK - 1) / G_BK;
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s) dma(s, s);
+#pragma unroll 1
+  for (int s = 0; s < nk; ++s) {
+    g_wait_vm<(NS - 2) * LPT>();  // K-step s has landed
+    __syncthreads();              // ... for every wavefront; all are done with K-step s-1
+    dma(s + NS - 1, (s + NS - 1) % NS);
+    const unsigned char* sb = lds + (s % NS) * STAGE;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      bf16x8 af[TM], bfr[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const bf16x8*>(sb + afo[i][ks]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        if constexpr (BT) {
+          bfr[j] = *reinterpret_cast<const bf16x8*>(sb + bfo[j][ks][0]);
+        } else {
+          typedef short shortx4 __attribute__((ext_vector_type(4)));
+          typedef __attribute__((address_space(3))) shortx4 lds_s4;
+          const shortx4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(sb + bfo[j][ks][0]));
+          const shortx4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(sb + bfo[j][ks][1]));
+          bfr[j] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = MF::mma(af[i], bfr[j], acc[i][j]);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the copies of K-steps past K have landed
+
+  // Epilogue: accumulator element e of tile (i, j) is C[row][col] with
+  // row = 8 * (e / 4) + 4 * (lane / 32) + e % 4, col = lane % 32.
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = n0 + wn * WN + j * 32 + lr;
+      if (col >= p.N) continue;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = m0 + wm * WM + i * 32 + 8 * (e / 4) + 4 * lg + (e % 4);
+        if (row < p.M) {
+          float vv = acc[i][j][e];
+          if (R) vv += to_f32(R[(long)row * p.ldr + col]);
+          C[(long)row * p.ldc + col] = from_f32<TO>(vv);
+        }
+      }
+    }
+}
+
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 template <typename T, typename TO, bool BT>
@@ -254,6 +475,24 @@ static int gemm_dispatch(const GemmArgs& a, int batch, int variant, hipStream_t 
   // Largest tile that still gives every CU a workgroup; 64x64 otherwise.
   const long t128 = (long)((a.M + 127) / 128) * ((a.N + 127) / 128) * batch;
   const long t64x128 = (long)((a.M + 63) / 64) * ((a.N + 127) / 128) * batch;
+  if constexpr (std::is_same<T, bf16>::value) {
+    // bf16: the LDS-DMA kernel, whose buffer offsets need operands under 2 GB.
+    const long a_bytes = 2L * ((long)(a.M - 1) * a.lda + a.K), b_bytes = BT ? 2L * ((long)(a.N - 1) * a.ldb + a.K)
+                                                                        : 2L * ((long)(a.K - 1) * a.ldb + a.N);
+    if (a_bytes < (1L << 31) && b_bytes < (1L << 31)) {
+      if (t128 >= 256) {
+        const long tiles = (long)((a.M + 127) / 128) * ((a.N + 127) / 128);
+        gemm_dma_kernel<TO, 128, 128, BT, 4><<<dim3((unsigned)tiles, 1, batch), dim3(256), 0, st>>>(a);
+      } else if (t64x128 >= 256) {
+        const long tiles = (long)((a.M + 63) / 64) * ((a.N + 127) / 128);
+        gemm_dma_kernel<TO, 64, 128, BT, 6><<<dim3((unsigned)tiles, 1, batch), dim3(256), 0, st>>>(a);
+      } else {
+        const long tiles = (long)((a.M + 63) / 64) * ((a.N + 63) / 64);
+        gemm_dma_kernel<TO, 64, 64, BT, 8><<<dim3((unsigned)tiles, 1, batch), dim3(256), 0, st>>>(a);
+      }
+      return check_launch("nkl_gemm(blocked)");
+    }
+  }
   if (t128 >= 256) {
     const long tiles = (long)((a.M + 127) / 128) * ((a.N + 127) / 128);
     gemm_blocked_kernel<T, TO, 128, 128, BT><<<dim3((unsigned)tiles, 1, batch), dim3(256), 0, st>>>(a);
