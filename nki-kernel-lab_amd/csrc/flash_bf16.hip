@@ -83,13 +83,7 @@ struct Layout {
   static constexpr int SLOT = 64 * 4 * (NCO + 1);          // floats of one wavefront's state
   static constexpr int PART = WPT * SLOT;                  // floats of one partial block state
   static constexpr int XBYTES = NT * WPT * SLOT * 4;       // team hand-over area (reuses the stages)
-  // With two teams the main loop is staggered (see the kernel) and the Q
-  // fragments are read from LDS, after the stages, instead of held in VGPRs.
-  static constexpr bool STAGGER = NT == 2;
-  static constexpr int LDQ = D + 8;                        // Q row stride (as K's)
-  static constexpr int QOFF = TOTAL;                       // Q block, [QB][LDQ]
-  static constexpr int LOOP = STAGGER ? TOTAL + QB * LDQ : TOTAL;
-  static constexpr int SMEM = LOOP * 2 > XBYTES ? LOOP : XBYTES / 2;  // bf16 elements of LDS
+  static constexpr int SMEM = TOTAL * 2 > XBYTES ? TOTAL : XBYTES / 2;  // bf16 elements of LDS
 };
 
 struct Work {
@@ -177,7 +171,6 @@ __global__ __launch_bounds__(64 * WPT * NT) void flash_bf16_kernel(AttnArgs p, W
   }
   // Per-lane LDS element offsets of the MFMA operands within a stage.
   const int kfrag_off = l32 * L::LDK + 8 * h32;
-  const int qfrag_off = L::QOFF + (32 * wq + l32) * L::LDQ + 8 * h32;  // this lane's Q row in LDS
   const int i16 = lane & 15, g2 = (lane >> 4) & 1;
   const int vfrag_off = L::K_ELEMS + (4 * h32 + (i16 >> 2)) * L::LDV + 16 * g2 + 4 * (i16 & 3);
 
@@ -289,12 +282,6 @@ __global__ __launch_bounds__(64 * WPT * NT) void flash_bf16_kernel(AttnArgs p, W
     const int nit = (t1 - t0 + NT - 1) / NT;
 
     lstore(0, rk, rv);
-    if constexpr (L::STAGGER) {
-      if (team == 0) {  // both teams work on the same queries: one copy
-#pragma unroll
-        for (int f = 0; f < NQF; ++f) *reinterpret_cast<bf16x8*>(smem + qfrag_off + 16 * f) = qf[f];
-      }
-    }
     __syncthreads();
     gload(cur, 1, p.k, p.k_sh, p.k_ss, goff_k, rk);
     gload(cur, 1, p.v, p.v_sh, p.v_ss, goff_v, rv);
@@ -363,64 +350,7 @@ __global__ __launch_bounds__(64 * WPT * NT) void flash_bf16_kernel(AttnArgs p, W
       }
     };
 
-    if constexpr (L::STAGGER) {
-      // Two phases per tile i, each ended by a barrier:
-      //   M(i)  O += P(i-1) V(i-1), then S(i) = K(i) Q^T            (MFMA)
-      //   V(i)  softmax of S(i) into P(i); tile i+1 from registers to
-      //         LDS stage (i+1) & 1; tile i+2 loaded into the registers (VALU)
-      // Teams of the second half run one phase behind, so that on every SIMD
-      // (which holds one wavefront of each half) one wavefront is in an M phase
-      // while the other is in a V phase.  Stage (i+1) & 1 was last read in M(i),
-      // one barrier before V(i) writes it; K(i+1) written in V(i) is read in
-      // M(i+1), one barrier later.
-      // Both halves run the same straight-line body; the lagging half takes
-      // one extra barrier first, the leading half one extra at the end.
-      const bool lagged = team >= NT / 2;
-      floatx16 sacc;
-      bf16x8 pf[2];
-      bool act_prev = false;  // tile i-1 was computed (P valid)
-      if (lagged) __syncthreads();
-#pragma unroll 1
-      for (int i = 0; i < nit; ++i) {
-        // ---- M(i)
-        if (act_prev) pv(team_base + ((i - 1) & 1) * L::STAGE, pf);  // O += P(i-1) V(i-1)
-        __builtin_amdgcn_sched_barrier(0);  // V(i-1) fragments die before K(i)'s are read
-        const int tj = t0 + team + NT * i;
-        // inside the segment and not above the diagonal (uniform over the wavefront)
-        const bool act = __builtin_amdgcn_readfirstlane(tj < t1 && tj * BN <= qw + 31);
-        if (act) {  // S(i) = K(i) Q^T
-          const bf16* sb = team_base + (i & 1) * L::STAGE;
-#pragma unroll
-          for (int e = 0; e < 16; ++e) sacc[e] = 0.f;
-          // K and Q fragments four at a time, read before their MFMAs
-          constexpr int FG = NQF >= 4 ? 4 : NQF;
-#pragma unroll
-          for (int f0 = 0; f0 < NQF; f0 += FG) {
-            bf16x8 kf[FG], qq[FG];
-#pragma unroll
-            for (int f = 0; f < FG; ++f) {
-              kf[f] = load_frag(sb + kfrag_off + 16 * (f0 + f));
-              qq[f] = load_frag(smem + qfrag_off + 16 * (f0 + f));
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int f = 0; f < FG; ++f) sacc = MF::mma(kf[f], qq[f], sacc);
-          }
-        }
-        __syncthreads();
-        // ---- V(i)
-        if (act) softmax(tj * BN, sacc, pf);
-        act_prev = act;
-        lstore((i + 1) & 1, rk, rv);
-        gload(cur, i + 2, p.k, p.k_sh, p.k_ss, goff_k, rk);
-        gload(cur, i + 2, p.v, p.v_sh, p.v_ss, goff_v, rv);
-        __syncthreads();
-      }
-      // ---- M(nit): the last tile's P V
-      if (act_prev) pv(team_base + ((nit - 1) & 1) * L::STAGE, pf);
-      __syncthreads();
-      if (!lagged) __syncthreads();
-    } else {
+    {
       // One step per tile: tile it computes from LDS stage it & 1; tile it + 1
       // (in registers since the previous step) is written to the other stage;
       // after the barrier tile it + 2 is loaded into the registers.
