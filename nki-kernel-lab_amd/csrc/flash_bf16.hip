@@ -549,8 +549,12 @@ __global__ __launch_bounds__(64 * WPT * NT) void flash_bf16_kernel(AttnArgs p, W
 
 // ------------------------------------------------- one wavefront per SIMD --
 //
-// The same unit schedules with 128-query blocks and d in (64, 128], as one
-// team of 4 wavefronts (one per SIMD), each holding 512 registers.  The
+// The same unit schedules for d in (64, 128], with every wavefront alone on
+// its SIMD (512 registers: O in AGPRs, Q in VGPRs).  A wavefront owns QW = 32
+// or 64 queries (one or two 32-query halves): with 64, every K and V fragment
+// read from LDS feeds two MFMAs, which halves the LDS read traffic per FLOP.
+// A workgroup of NW wavefronts takes blocks of QB = QW * NW queries; with
+// NW = 2 two workgroups share a CU.  The
 // wavefront overlaps its own MFMA and VALU work: the QK^T MFMAs of tile i+1
 // are issued before the softmax and P V of tile i.  K/V tiles are copied
 // global -> LDS by the buffer unit (buffer_load ... lds: lane l's 16 bytes
@@ -570,7 +574,6 @@ constexpr int W1_NS = 4;                    // LDS stages (offsets stay below 64
 constexpr int W1_ROWB = 256;                // bytes of a K/V row (d = 128)
 constexpr int W1_TILEB = BN * W1_ROWB;      // bytes of a K (or V) tile
 constexpr int W1_STAGEB = 2 * W1_TILEB;     // K tile then V tile
-constexpr int W1_LPT = 4;                   // DMA instructions per tile per wavefront (2 K + 2 V)
 
 __device__ __forceinline__ int w1_swz(int r) { return ((r & 3) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1); }
 
@@ -583,10 +586,16 @@ __device__ __forceinline__ void wait_vm() {
 
 }  // namespace
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+template <int QH, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void flash_bf16_w1_kernel(AttnArgs p, Work w) {
-  constexpr int D = 128, NQF = D / 16, NDB = D / 32, QB = 128, WPT = 4;
-  constexpr int NCO = 4 * NDB, SLOT = 64 * 4 * (NCO + 1), PART = WPT * SLOT;
+  static_assert((QH == 1 || QH == 2) && (NW == 2 || NW == 4), "32 or 64 queries per wavefront, 2 or 4 wavefronts");
+  constexpr int D = 128, NQF = D / 16, NDB = D / 32, QW = 32 * QH, QB = QW * NW;
+  // Partial state of one 32-query half: NCO float4 chunks of O and one of
+  // (m, l) per lane.
+  constexpr int NCO = 4 * NDB, HS = 64 * 4 * (NCO + 1), SLOT = QH * HS, PART = NW * SLOT;
+  constexpr int NI = 8 / NW;    // 1 KB copies per K (and per V) tile per wavefront
+  constexpr int LPT = 2 * NI;   // copies per tile per wavefront
   using MF = Mfma32<bf16>;
   __shared__ __align__(16) unsigned char lds[W1_NS * W1_STAGEB];
   __shared__ int arrival;
@@ -623,13 +632,15 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
         voff[db][half] = W1_TILEB + row * W1_ROWB + (((4 * db + cb) ^ w1_swz(row)) << 4) + (i16 & 1) * 8;
       }
   }
-  //   DMA: this wavefront copies rows 8 wq .. 8 wq + 7 of each tile, as two
-  //   1 KB instructions n = 2 wq + u (rows 4 n .. 4 n + 3); lane l fills
-  //   row 4 n + l / 16, physical chunk l % 16.  Chunks past d read as zero.
-  int dk[2], dv[2];
+  //   DMA: this wavefront copies rows 4 NI wq .. 4 NI (wq + 1) - 1 of each
+  //   tile, as NI 1 KB instructions n = NI wq + u (rows 4 n .. 4 n + 3); lane l
+  //   fills row 4 n + l / 16, physical chunk l % 16.  Chunks past d read as zero.
+  // The first NI entries are used.  (With a size that depends on the template
+  // parameters, hipcc emitted no host launch stub for the kernel.)
+  int dk[4], dv[4];
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int row = 4 * (2 * wq + u) + (lane >> 4);
+  for (int u = 0; u < NI; ++u) {
+    const int row = 4 * (NI * wq + u) + (lane >> 4);
     const int lc = (lane & 15) ^ w1_swz(row);
     const bool ok = lc * 8 < dlim;
     dk[u] = ok ? 2 * (row * (int)p.k_ss + lc * 8) : 0x40000000;
@@ -689,14 +700,17 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
     sg.t1 = (int)(min(u1, sg.bstart + sg.nt) - sg.bstart);
     return sg;
   };
-  bf16x8 qf[NQF];
+  bf16x8 qf[QH][NQF];
   auto load_q = [&](const Seg& sg) __attribute__((always_inline)) {
     const bf16* Q = static_cast<const bf16*>(p.q) + (long)sg.hh * p.q_sh;
-    const int qrow = QB * sg.b + 32 * wq + l32;
 #pragma unroll
-    for (int f = 0; f < NQF; ++f) {
-      const int dd = 16 * f + 8 * h32;
-      qf[f] = __builtin_bit_cast(bf16x8, ld16_or_zero(Q, (long)qrow * p.q_ss + dd, qrow < S && dd < dlim));
+    for (int hq = 0; hq < QH; ++hq) {
+      const int qrow = QB * sg.b + QW * wq + 32 * hq + l32;
+#pragma unroll
+      for (int f = 0; f < NQF; ++f) {
+        const int dd = 16 * f + 8 * h32;
+        qf[hq][f] = __builtin_bit_cast(bf16x8, ld16_or_zero(Q, (long)qrow * p.q_ss + dd, qrow < S && dd < dlim));
+      }
     }
   };
   // Copies tile j (0-based within the segment) of K and V into LDS stage st;
@@ -715,8 +729,8 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
         kBufferFlags);
     unsigned char* sb = lds + st * W1_STAGEB;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int n = 2 * wq + u;
+    for (int u = 0; u < NI; ++u) {
+      const int n = NI * wq + u;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(sb + n * 1024), 16,
                                                dk[u], 0, 0, 0);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(sb + W1_TILEB + n * 1024),
@@ -730,21 +744,25 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
   for (;;) {
     const int hh = cur.hh, b = cur.b, t0 = cur.t0, t1 = cur.t1, nt_b = cur.nt;
     const long bstart = cur.bstart;
-    const int qw = QB * b + 32 * wq;
-    const int myq = qw + l32;
+    const int qw = QB * b + QW * wq;  // first query of this wavefront
     const int nt = t1 - t0;
 
 #pragma unroll
     for (int j = 0; j < W1_NS - 1; ++j) dma(cur, j, j);
-    wait_vm<(W1_NS - 2) * W1_LPT>();  // tile 0 has landed (and Q)
+    wait_vm<(W1_NS - 2) * LPT>();  // tile 0 has landed (and Q)
     __syncthreads();
 
-    float m_run = -INFINITY, l_run = 0.f;
-    floatx16 oacc[NDB];
+    float m_run[QH], l_run[QH];
+    floatx16 oacc[QH][NDB];
 #pragma unroll
-    for (int db = 0; db < NDB; ++db)
+    for (int hq = 0; hq < QH; ++hq) {
+      m_run[hq] = -INFINITY;
+      l_run[hq] = 0.f;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) oacc[db][e] = 0.f;
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) oacc[hq][db][e] = 0.f;
+    }
 
     // Software pipeline, per tile i (two scheduling regions, each a
     // fixed interleave of MFMA and VALU instructions):
@@ -755,9 +773,9 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
     // segment are masked to -inf, so a tile wholly above a wavefront's
     // diagonal contributes exact zeros.
     const int klim_seg = (t0 + nt) * BN;  // keys at or past this are outside the segment
-    auto mask_max = [&](int j, floatx16& sc) __attribute__((always_inline)) {
+    auto mask_max = [&](int j, int hq, floatx16& sc) __attribute__((always_inline)) {
       const int k0 = (t0 + j) * BN;
-      const int lim = min(myq, klim_seg - 1);  // last key this query may see in the segment
+      const int lim = min(qw + 32 * hq + l32, klim_seg - 1);  // last key this query may see in the segment
       float mx = -INFINITY;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
@@ -773,24 +791,43 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
       return mx;
     };
     // Tile j needs masking when it reaches past this wavefront's first query
-    // or lies outside the segment (uniform over the wavefront).
-    auto needs_mask = [&](int j) __attribute__((always_inline)) {
-      return (bool)__builtin_amdgcn_readfirstlane(j >= nt || (t0 + j) * BN + BN - 1 > qw);
-    };
-    // Raises the running max when the tile's max exceeds it by the slack
+    // (tile index t0 + j >= qw / BN) or lies outside the segment; the tiles
+    // j >= jm of the segment do.  jm is uniform over the wavefront.
+    const int jm = __builtin_amdgcn_readfirstlane(max(0, min(nt, qw / BN - t0)));
+    // Raises the running maxima when a tile's max exceeds one by the slack
     // (rescaling O and l after the P V of the previous tile).
-    auto rescale = [&](float mx) __attribute__((always_inline)) {
-      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave)) * c;
-      if (__builtin_amdgcn_ballot_w64(mx > m_run + kRescaleSlack)) {
-        const float m_new = fmaxf(m_run, mx);
-        const float corr = m_run == -INFINITY ? 0.f : fast_exp2(m_run - m_new);
-        m_run = m_new;
-        l_run *= corr;
+    auto rescale = [&](float (&mx)[QH]) __attribute__((always_inline)) {
+      bool up = false;
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) oacc[db][e] *= corr;
+      for (int hq = 0; hq < QH; ++hq) {
+        mx[hq] = fmaxf(mx[hq], __shfl_xor(mx[hq], 32, kWave)) * c;
+        up = up || mx[hq] > m_run[hq] + kRescaleSlack;
       }
+      if (__builtin_amdgcn_ballot_w64(up)) {
+#pragma unroll
+        for (int hq = 0; hq < QH; ++hq) {
+          const float m_new = fmaxf(m_run[hq], mx[hq]);
+          const float corr = m_run[hq] == -INFINITY ? 0.f : fast_exp2(m_run[hq] - m_new);
+          m_run[hq] = m_new;
+          l_run[hq] *= corr;
+#pragma unroll
+          for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) oacc[hq][db][e] *= corr;
+        }
+      }
+    };
+    // exp2 of scaled scores e0 .. e1 - 1 of half hq, added to the row sum.
+    auto expo = [&](floatx16& sc, float mneg, float& rs, int e0, int e1) __attribute__((always_inline)) {
+#pragma unroll
+      for (int e = e0; e < e1; ++e) {
+        sc[e] = fast_exp2(fmaf(sc[e], c, mneg));
+        rs += sc[e];
+      }
+    };
+    auto to_p = [&](const floatx16& sc, int uu, bf16x8& pf) __attribute__((always_inline)) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pf[j] = (bf16)sc[8 * uu + j];
     };
     auto kfrags = [&](int st, bf16x8 (&kf)[NQF]) __attribute__((always_inline)) {
       const unsigned char* sb = lds + st * W1_STAGEB;
@@ -811,119 +848,166 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
         }
     };
 
-    floatx16 s0, s1;
+    auto pv = [&](int hq, const bf16x8 (&va)[NDB][2], const bf16x8 (&pf)[2]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int uu = 0; uu < 2; ++uu) oacc[hq][db] = MF::mma(va[db][uu], pf[uu], oacc[hq][db]);
+    };
+
+    floatx16 s0[QH], s1[QH];
     {  // S(0), its mask, max and rescale
       bf16x8 kf[NQF];
       kfrags(0, kf);
+      const bool msk = jm == 0;
+      float mx[QH];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) s0[e] = 0.f;
+      for (int hq = 0; hq < QH; ++hq) {
 #pragma unroll
-      for (int f = 0; f < NQF; ++f) s0 = MF::mma(kf[f], qf[f], s0);
-      rescale(needs_mask(0) ? mask_max(0, s0) : plain_max(s0));
+        for (int e = 0; e < 16; ++e) s0[hq][e] = 0.f;
+#pragma unroll
+        for (int f = 0; f < NQF; ++f) s0[hq] = MF::mma(kf[f], qf[hq][f], s0[hq]);
+        mx[hq] = msk ? mask_max(0, hq, s0[hq]) : plain_max(s0[hq]);
+      }
+      rescale(mx);
     }
-    auto step = [&](int i, int st, floatx16& sc, floatx16& sn) __attribute__((always_inline)) {
+    // Software pipeline, per tile i.  With one half (32 queries):
+    //   region 1: S(i+1) = K(i+1) Q^T     x  exp, row sums, bf16 P(i)
+    //   region 2: O += P(i) V(i)          x  mask and row max of S(i+1)
+    // With two halves the exp work of S(i) is spread over the QK MFMAs and the
+    // P V MFMAs of half 0, which need only half 0's P:
+    //   region 1: S(i+1), both halves     x  exp of half 0, first 8 keys of half 1
+    //   region 2: O(half 0) += P V        x  exp of half 1's last 8 keys
+    //   region 3: O(half 1) += P V        x  mask and row max of S(i+1)
+    // A step either masks S(i+1) or does not (a compile-time choice), so that
+    // no branch separates MFMAs that update O and every P V updates O in place.
+    auto step = [&](auto masked, int i, int st, floatx16 (&sc)[QH], floatx16 (&sn)[QH])
+                    __attribute__((always_inline)) {
+      constexpr bool MSK = decltype(masked)::value;
       const int st1 = (st + 1) % W1_NS, stp = (st + W1_NS - 1) % W1_NS;
-      wait_vm<(W1_NS - 3) * W1_LPT>();  // tile i+1 has landed
-      __syncthreads();                  // ... for every wavefront; all are done with tile i-1
-      dma(cur, i + W1_NS - 1, stp);     // into tile i-1's stage
+      wait_vm<(W1_NS - 3) * LPT>();  // tile i+1 has landed
+      __syncthreads();               // ... for every wavefront; all are done with tile i-1
+      dma(cur, i + W1_NS - 1, stp);  // into tile i-1's stage
       bf16x8 kf[NQF], va[NDB][2];
       kfrags(st1, kf);  // every fragment read of the tile is in flight
       vfrags(st, va);   // before the first MFMA waits for one
-      const bool msk = needs_mask(i + 1);
       __builtin_amdgcn_sched_barrier(0);
-      // ---- region 1: S(i+1) MFMAs x exp / sums / P(i)
-      const float mneg = m_run == -INFINITY ? 0.f : -m_run;  // an empty row keeps exp2(-inf) = 0
+      float mneg[QH], rs[QH];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) sn[e] = 0.f;
-      float rs = 0.f;
-      bf16x8 pf[2];
+      for (int hq = 0; hq < QH; ++hq) {
+        mneg[hq] = m_run[hq] == -INFINITY ? 0.f : -m_run[hq];  // an empty row keeps exp2(-inf) = 0
+        rs[hq] = 0.f;
 #pragma unroll
-      for (int f = 0; f < NQF; ++f) {
-        sn = MF::mma(kf[f], qf[f], sn);
+        for (int e = 0; e < 16; ++e) sn[hq][e] = 0.f;
+      }
+      bf16x8 pf[QH][2];
+      // ---- region 1
 #pragma unroll
-        for (int e = 2 * f; e < 2 * f + 2; ++e) {
-          sc[e] = fast_exp2(fmaf(sc[e], c, mneg));
-          rs += sc[e];
+      for (int f = 0; f < NQF; ++f)
+#pragma unroll
+        for (int hq = 0; hq < QH; ++hq) sn[hq] = MF::mma(kf[f], qf[hq][f], sn[hq]);
+      expo(sc[0], mneg[0], rs[0], 0, 16);
+      to_p(sc[0], 0, pf[0][0]);
+      to_p(sc[0], 1, pf[0][1]);
+      if constexpr (QH == 2) {
+        expo(sc[1], mneg[1], rs[1], 0, 8);
+        to_p(sc[1], 0, pf[1][0]);
+      }
+#pragma unroll
+      for (int f = 0; f < NQF * QH; ++f) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);             // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, QH == 1 ? 6 : 5, 0);  // VALU
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (QH == 2) {
+        // ---- region 2
+        pv(0, va, pf[0]);
+        expo(sc[1], mneg[1], rs[1], 8, 16);
+        to_p(sc[1], 1, pf[1][1]);
+#pragma unroll
+        for (int k = 0; k < 2 * NDB; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 3);
+          __builtin_amdgcn_sched_group_barrier(0x002, 4, 3);
         }
+        __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
-      for (int uu = 0; uu < 2; ++uu)
+      for (int hq = 0; hq < QH; ++hq) l_run[hq] += rs[hq];
+      // ---- last region: P V of the last half x (mask and) max of S(i+1)
+      float mx[QH];
+      pv(QH - 1, va, pf[QH - 1]);
+      if constexpr (MSK) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) pf[uu][j] = (bf16)sc[8 * uu + j];
-      l_run += rs;
-#pragma unroll
-      for (int f = 0; f < NQF; ++f) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // six VALU
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      // ---- region 2: O += P(i) V(i) x (mask and) max of S(i+1)
-      float mx;
-      if (msk) {
-#pragma unroll
-        for (int db = 0; db < NDB; ++db)
-#pragma unroll
-          for (int uu = 0; uu < 2; ++uu) oacc[db] = MF::mma(va[db][uu], pf[uu], oacc[db]);
-        mx = mask_max(i + 1, sn);
+        for (int hq = 0; hq < QH; ++hq) mx[hq] = mask_max(i + 1, hq, sn[hq]);
 #pragma unroll
         for (int k = 0; k < 2 * NDB; ++k) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-          __builtin_amdgcn_sched_group_barrier(0x002, 5, 1);
+          __builtin_amdgcn_sched_group_barrier(0x002, 5 * QH, 1);
         }
-        __builtin_amdgcn_sched_barrier(0);
       } else {
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
-#pragma unroll
-          for (int uu = 0; uu < 2; ++uu) oacc[db] = MF::mma(va[db][uu], pf[uu], oacc[db]);
-        mx = plain_max(sn);
+        for (int hq = 0; hq < QH; ++hq) mx[hq] = plain_max(sn[hq]);
 #pragma unroll
         for (int k = 0; k < 2 * NDB; ++k) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 2);
-          __builtin_amdgcn_sched_group_barrier(0x002, 2, 2);
+          __builtin_amdgcn_sched_group_barrier(0x002, 2 * QH, 2);
         }
-        __builtin_amdgcn_sched_barrier(0);
       }
+      __builtin_amdgcn_sched_barrier(0);
       rescale(mx);
     };
-    static_assert(W1_NS == 4, "the loop below is unrolled by the stage count");
+    // Steps i whose S(i+1) needs no mask (i + 1 < jm) run four at a time from
+    // stage 0; the rest mask every tile.
+    static_assert(W1_NS == 4, "the loops below are unrolled by the stage count");
+    constexpr std::integral_constant<bool, false> kPlain{};
+    constexpr std::integral_constant<bool, true> kMasked{};
+    int i = 0;
 #pragma unroll 1
-    for (int i = 0; i < nt; i += 4) {
-      step(i, 0, s0, s1);
-      if (i + 1 >= nt) break;
-      step(i + 1, 1, s1, s0);
-      if (i + 2 >= nt) break;
-      step(i + 2, 2, s0, s1);
-      if (i + 3 >= nt) break;
-      step(i + 3, 3, s1, s0);
+    for (; i + 4 < jm; i += 4) {
+      step(kPlain, i, 0, s0, s1);
+      step(kPlain, i + 1, 1, s1, s0);
+      step(kPlain, i + 2, 2, s0, s1);
+      step(kPlain, i + 3, 3, s1, s0);
+    }
+#pragma unroll 1
+    for (; i < nt; ++i) {  // one step per iteration (stage from i, S(i+1) moved into s0)
+      step(kMasked, i, i & (W1_NS - 1), s0, s1);
+#pragma unroll
+      for (int hq = 0; hq < QH; ++hq) s0[hq] = s1[hq];
     }
     __builtin_amdgcn_s_waitcnt(0);  // the copies of tiles past the segment have landed
     __syncthreads();
 
-    float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
-    auto weights = [&](float m2, float l2, float& a1, float& a2) __attribute__((always_inline)) {
-      const float M = fmaxf(m_run, m2);
-      a1 = m_run == -INFINITY ? 0.f : fast_exp2(m_run - M);
+    float l_tot[QH];
+#pragma unroll
+    for (int hq = 0; hq < QH; ++hq) l_tot[hq] = l_run[hq] + __shfl_xor(l_run[hq], 32, kWave);
+    auto weights = [&](int hq, float m2, float l2, float& a1, float& a2) __attribute__((always_inline)) {
+      const float M = fmaxf(m_run[hq], m2);
+      a1 = m_run[hq] == -INFINITY ? 0.f : fast_exp2(m_run[hq] - M);
       a2 = m2 == -INFINITY ? 0.f : fast_exp2(m2 - M);
-      l_tot = l_tot * a1 + l2 * a2;
-      m_run = M;
+      l_tot[hq] = l_tot[hq] * a1 + l2 * a2;
+      m_run[hq] = M;
     };
     auto store_out = [&]() __attribute__((always_inline)) {
-      const float linv = 1.0f / l_tot;
-      if (myq < S) {
-        bf16* orow = static_cast<bf16*>(p.o) + (long)hh * p.o_sh + (long)myq * p.o_ss;
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
+      for (int hq = 0; hq < QH; ++hq) {
+        const float linv = 1.0f / l_tot[hq];
+        const int myq = qw + 32 * hq + l32;
+        if (myq < S) {
+          bf16* orow = static_cast<bf16*>(p.o) + (long)hh * p.o_sh + (long)myq * p.o_ss;
 #pragma unroll
-          for (int bq = 0; bq < 4; ++bq) {
-            const int dd = 32 * db + 8 * bq + 4 * h32;
-            if (dd < dlim) {
-              float ov[4];
+          for (int db = 0; db < NDB; ++db)
 #pragma unroll
-              for (int e = 0; e < 4; ++e) ov[e] = oacc[db][4 * bq + e] * linv;
-              store_vec<4>(orow + dd, ov);
+            for (int bq = 0; bq < 4; ++bq) {
+              const int dd = 32 * db + 8 * bq + 4 * h32;
+              if (dd < dlim) {
+                float ov[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) ov[e] = oacc[hq][db][4 * bq + e] * linv;
+                store_vec<4>(orow + dd, ov);
+              }
             }
-          }
+        }
       }
     };
 
@@ -943,20 +1027,24 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
     } else {
       typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
       const __amdgpu_buffer_rsrc_t prsrc = __builtin_amdgcn_make_buffer_rsrc(w.part, (short)0, w.part_bytes, kBufferFlags);
-      auto poff = [&](int v, int s2, int k) __attribute__((always_inline)) {
-        return 4 * (((v * 2 + s2) * PART) + wq * SLOT + k * 256 + 4 * lane);
+      auto poff = [&](int v, int s2, int hq, int k) __attribute__((always_inline)) {
+        return 4 * (((v * 2 + s2) * PART) + wq * SLOT + hq * HS + k * 256 + 4 * lane);
       };
       const int slot = range_start(vidx, w) >= bstart ? 0 : 1;
 #pragma unroll
-      for (int db = 0; db < NDB; ++db)
+      for (int hq = 0; hq < QH; ++hq) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k)
-          __builtin_amdgcn_raw_buffer_store_b128(
-              __builtin_bit_cast(u32x4, make_float4(oacc[db][4 * k], oacc[db][4 * k + 1], oacc[db][4 * k + 2],
-                                                    oacc[db][4 * k + 3])),
-              prsrc, poff(vidx, slot, 4 * db + k), 0, kDeviceCoherent);
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, make_float4(m_run, l_tot, 0.f, 0.f)), prsrc,
-                                             poff(vidx, slot, NCO), 0, kDeviceCoherent);
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+            __builtin_amdgcn_raw_buffer_store_b128(
+                __builtin_bit_cast(u32x4, make_float4(oacc[hq][db][4 * k], oacc[hq][db][4 * k + 1],
+                                                      oacc[hq][db][4 * k + 2], oacc[hq][db][4 * k + 3])),
+                prsrc, poff(vidx, slot, hq, 4 * db + k), 0, kDeviceCoherent);
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(u32x4, make_float4(m_run[hq], l_tot[hq], 0.f, 0.f)), prsrc,
+            poff(vidx, slot, hq, NCO), 0, kDeviceCoherent);
+      }
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
       if (tid == 0) arrival = atomicAdd(&w.count[hh * w.nqb + b], 1);
@@ -967,22 +1055,30 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
         for (int v2 = vf; v2 < vf + nparts; ++v2) {
           if (v2 == vidx) continue;
           const int slot2 = range_start(v2, w) >= bstart ? 0 : 1;
-          float4 v[NCO + 1];
 #pragma unroll
-          for (int k = 0; k <= NCO; ++k)
-            v[k] = __builtin_bit_cast(float4,
-                                      __builtin_amdgcn_raw_buffer_load_b128(prsrc, poff(v2, slot2, k), 0, kDeviceCoherent));
-          float a1, a2;
-          weights(v[NCO].x, v[NCO].y, a1, a2);
+          for (int hq = 0; hq < QH; ++hq) {
+            // (m, l) first, then O one d-block (4 float4 per lane) at a time.
+            const float4 ml = __builtin_bit_cast(
+                float4, __builtin_amdgcn_raw_buffer_load_b128(prsrc, poff(v2, slot2, hq, NCO), 0, kDeviceCoherent));
+            float a1, a2;
+            weights(hq, ml.x, ml.y, a1, a2);
 #pragma unroll
-          for (int db = 0; db < NDB; ++db)
+            for (int db = 0; db < NDB; ++db) {
+              float4 v[4];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-              oacc[db][4 * k] = fmaf(v[4 * db + k].x, a2, oacc[db][4 * k] * a1);
-              oacc[db][4 * k + 1] = fmaf(v[4 * db + k].y, a2, oacc[db][4 * k + 1] * a1);
-              oacc[db][4 * k + 2] = fmaf(v[4 * db + k].z, a2, oacc[db][4 * k + 2] * a1);
-              oacc[db][4 * k + 3] = fmaf(v[4 * db + k].w, a2, oacc[db][4 * k + 3] * a1);
+              for (int k = 0; k < 4; ++k)
+                v[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      prsrc, poff(v2, slot2, hq, 4 * db + k), 0, kDeviceCoherent));
+#pragma unroll
+              for (int k = 0; k < 4; ++k) {
+                floatx16& o = oacc[hq][db];
+                o[4 * k] = fmaf(v[k].x, a2, o[4 * k] * a1);
+                o[4 * k + 1] = fmaf(v[k].y, a2, o[4 * k + 1] * a1);
+                o[4 * k + 2] = fmaf(v[k].z, a2, o[4 * k + 2] * a1);
+                o[4 * k + 3] = fmaf(v[k].w, a2, o[4 * k + 3] * a1);
+              }
             }
+          }
         }
         store_out();
         if (tid == 0) atomicExch(&w.count[hh * w.nqb + b], 0);
@@ -1005,12 +1101,22 @@ int cu_count() {
   return n;
 }
 
-// A launch configuration: queries per block (64: 2 wavefronts x 4 teams;
-// 128: 4 wavefronts x 2 teams) and a schedule.
+// Kernels: teams of wavefronts sharing SIMDs, or one wavefront per SIMD with
+// 32 queries (4 per workgroup) or 64 queries (2 or 4 per workgroup).
+enum Kern { kTeams = 0, kW32x4 = 1, kW64x2 = 2, kW64x4 = 3 };
+
+// A launch configuration: queries per block, a schedule and a kernel.  The
+// teams kernel takes 64-query blocks (2 wavefronts x 4 teams) or 128-query
+// blocks (4 wavefronts x 2 teams); the others take 32 or 64 queries per
+// wavefront times their wavefront count.
 struct Config {
   int qb;
   int sched;
+  int kern;
 };
+
+// Resident workgroups per CU: two for the two-wavefront kernel, else one.
+int wgs_per_cu(int kern) { return kern == kW64x2 ? 2 : 1; }
 
 Work plan(int H, int S, Config cfg) {
   Work w{};
@@ -1022,11 +1128,11 @@ Work plan(int H, int S, Config cfg) {
   w.sched = cfg.sched;
   w.paired = cfg.sched != kBlock;
   if (cfg.sched == kBalanced) {
-    // At most one workgroup per CU, and no range shorter than kMinUnits: a
-    // short range spends most of its time filling the pipeline, and splits a
-    // block into many parts for its last workgroup to merge.
+    // As many workgroups as are resident at once, and no range shorter than
+    // kMinUnits: a short range spends most of its time filling the pipeline,
+    // and splits a block into many parts for its last workgroup to merge.
     const long by_size = (w.units + kMinUnits - 1) / kMinUnits;
-    const int cus = cu_count();
+    const int cus = cu_count() * wgs_per_cu(cfg.kern);
     w.grid = (int)(by_size < cus ? by_size : cus);
   } else if (cfg.sched == kPairs) {
     w.grid = H * ((w.nqb + 1) / 2);
@@ -1041,15 +1147,16 @@ Work plan(int H, int S, Config cfg) {
 // every CU busy; up to ~1000 units per CU the balanced schedule wins (whole
 // blocks leave CUs idle or unevenly loaded); beyond that one workgroup per
 // pair of blocks balances as well and needs no partial states.
-// NKL_FLASH_SCHEDULE=block|pairs|balanced and NKL_FLASH_QB=64|128 override
-// the choice (tests, tuning).
-Config choose(int H, int S) {
+// NKL_FLASH_SCHEDULE=block|pairs|balanced, NKL_FLASH_QB=64|128 and
+// NKL_FLASH_KERNEL=teams|w1|w64|w64x4 override the choice (tests, tuning);
+// the one-wavefront-per-SIMD kernels take 64 < d <= 128 and fix the block.
+Config choose(int H, int S, int d) {
   const long cus = cu_count();
   const long nqb = (S + 127) / 128;
   const long units128 = (long)H * (2 * (nqb - 1) * nqb + (S - 1) / BN + 1);
-  Config cfg = units128 < 12 * cus ? Config{64, kBalanced}
-               : units128 < 1024 * cus ? Config{128, kBalanced}
-                                       : Config{128, kPairs};
+  Config cfg = units128 < 12 * cus ? Config{64, kBalanced, kTeams}
+               : units128 < 1024 * cus ? Config{128, kBalanced, kTeams}
+                                       : Config{128, kPairs, kTeams};
   if (const char* f = getenv("NKL_FLASH_SCHEDULE")) {
     if (!strcmp(f, "block")) cfg.sched = kBlock;
     if (!strcmp(f, "pairs")) cfg.sched = kPairs;
@@ -1059,12 +1166,24 @@ Config choose(int H, int S) {
     if (!strcmp(f, "64")) cfg.qb = 64;
     if (!strcmp(f, "128")) cfg.qb = 128;
   }
+  if (const char* f = getenv("NKL_FLASH_KERNEL")) {
+    if (!strcmp(f, "teams")) cfg.kern = kTeams;
+    if (!strcmp(f, "w1")) cfg.kern = kW32x4;
+    if (!strcmp(f, "w64")) cfg.kern = kW64x2;
+    if (!strcmp(f, "w64x4")) cfg.kern = kW64x4;
+  }
+  if (d <= 64) cfg.kern = kTeams;
+  if (cfg.kern == kW32x4 || cfg.kern == kW64x2) cfg.qb = 128;
+  if (cfg.kern == kW64x4) cfg.qb = 256;
   return cfg;
 }
 
+// Floats of one workgroup's partial state (one of its two slots).  Every
+// kernel stores (O, m, l) of each 32-query group as 4 * (d / 8 + 1) float4
+// per lane, so the size depends on the block only.
 template <int D>
 size_t part_floats(int qb) {
-  return qb == 64 ? Layout<D, 2, 4>::PART : Layout<D, 4, 2>::PART;
+  return qb == 64 ? Layout<D, 2, 4>::PART : (size_t)(qb / 128) * Layout<D, 4, 2>::PART;
 }
 
 size_t part_floats_for(int d, int qb) {
@@ -1074,6 +1193,11 @@ size_t part_floats_for(int d, int qb) {
 template <int D, int WPT, int NT>
 void launch(const AttnArgs& a, const Work& w, hipStream_t st) {
   flash_bf16_kernel<D, WPT, NT><<<dim3((unsigned)w.grid), dim3(64 * WPT * NT), 0, st>>>(a, w);
+}
+
+template <int QH, int NW>
+void launch_w(const AttnArgs& a, const Work& w, hipStream_t st) {
+  flash_bf16_w1_kernel<QH, NW><<<dim3((unsigned)w.grid), dim3(64 * NW), 0, st>>>(a, w);
 }
 
 template <int D>
@@ -1088,26 +1212,27 @@ void launch_qb(const AttnArgs& a, const Work& w, int qb, hipStream_t st) {
 
 size_t flash_bf16_workspace_bytes(int H, int S, int d) {
   if (H <= 0 || S <= 0) return 0;
-  const Config cfg = choose(H, S);
+  const Config cfg = choose(H, S, d);
   if (cfg.sched != kBalanced) return 0;
   return (size_t)plan(H, S, cfg).grid * 2 * part_floats_for(d, cfg.qb) * 4;
 }
 
+// The counters do not depend on d: one per 64-query block (the smallest
+// block) whenever some head dim takes the balanced schedule for this shape.
 size_t flash_bf16_counter_bytes(int H, int S) {
   if (H <= 0 || S <= 0) return 0;
-  const Config cfg = choose(H, S);
-  if (cfg.sched != kBalanced) return 0;
-  return (size_t)H * plan(H, S, cfg).nqb * 4;
+  if (choose(H, S, 32).sched != kBalanced && choose(H, S, 128).sched != kBalanced) return 0;
+  return (size_t)H * ((S + 63) / 64) * 4;
 }
 
 int flash_bf16_launch(const AttnArgs& a, void* workspace, size_t workspace_bytes, int* counters,
                       size_t counter_bytes, hipStream_t st) {
-  Config cfg = choose(a.H, a.S);
+  Config cfg = choose(a.H, a.S, a.d);
   if (cfg.sched == kBalanced && !workspace) cfg.sched = kPairs;  // the plain entry point: no scratch
   Work w = plan(a.H, a.S, cfg);
   if (cfg.sched == kBalanced) {
     const size_t need = flash_bf16_workspace_bytes(a.H, a.S, a.d);
-    const size_t need_c = flash_bf16_counter_bytes(a.H, a.S);
+    const size_t need_c = (size_t)a.H * w.nqb * 4;
     if (workspace_bytes < need || !counters || counter_bytes < need_c)
       return set_error(NKL_EWORKSPACE,
                        "nkl_flash_attn_causal_ws: workspace of %zu bytes and counters of %zu bytes needed, "
@@ -1116,12 +1241,13 @@ int flash_bf16_launch(const AttnArgs& a, void* workspace, size_t workspace_bytes
     w.part_bytes = (int)need;
     w.count = counters;
   }
-  // The one-wavefront-per-SIMD kernel takes 128-query blocks with
-  // 64 < d <= 128; NKL_FLASH_KERNEL=w1|teams overrides.
-  bool w1 = false;
-  if (const char* f = getenv("NKL_FLASH_KERNEL")) w1 = !strcmp(f, "w1");
-  if (w1 && cfg.qb == 128 && a.d > 64) {
-    flash_bf16_w1_kernel<<<dim3((unsigned)w.grid), dim3(256), 0, st>>>(a, w);
+  if (cfg.kern != kTeams) {
+    if (cfg.kern == kW32x4)
+      launch_w<1, 4>(a, w, st);
+    else if (cfg.kern == kW64x2)
+      launch_w<2, 2>(a, w, st);
+    else
+      launch_w<2, 4>(a, w, st);
     return check_launch("nkl_flash_attn_causal");
   }
   if (a.d <= 32)

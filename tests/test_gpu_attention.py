@@ -135,21 +135,35 @@ def test_flash_bf16_schedules(rng, monkeypatch, qb, schedule, H, S, d):
     np.testing.assert_allclose(out[:, 0], _np(v)[:, 0], atol=1e-2)  # query 0 sees only key 0
 
 
+@pytest.mark.parametrize("kernel", ["w1", "w64", "w64x4"])
 @pytest.mark.parametrize("schedule", ["balanced", "pairs", "block"])
 @pytest.mark.parametrize("H,S,d", [(1, 1, 128), (3, 77, 128), (1, 300, 128), (2, 1537, 128), (5, 640, 96),
                                    (1, 129, 128), (2, 4096, 128), (4, 257, 72)])
-def test_flash_bf16_one_wave_per_simd_kernel(rng, monkeypatch, schedule, H, S, d):
-    """The 4-wavefront kernel (LDS-DMA staging, swizzled rows) under each schedule."""
+def test_flash_bf16_one_wave_per_simd_kernel(rng, monkeypatch, kernel, schedule, H, S, d):
+    """The one-wavefront-per-SIMD kernels (LDS-DMA staging, swizzled rows) under
+    each schedule: 32 queries x 4 wavefronts, 64 x 2 and 64 x 4."""
     from nkilab import ops
 
-    monkeypatch.setenv("NKL_FLASH_KERNEL", "w1")
+    monkeypatch.setenv("NKL_FLASH_KERNEL", kernel)
     monkeypatch.setenv("NKL_FLASH_SCHEDULE", schedule)
-    monkeypatch.setenv("NKL_FLASH_QB", "128")
     q, k, v = (_bf(rng.standard_normal((H, S, d))) for _ in range(3))
     out = _np(ops.attention(q, k, v))
     ref = _sdpa_cpu(*(_np(t) for t in (q, k, v)))
-    assert rel_err(out, ref) < 1e-2, (schedule, H, S, d)
+    assert rel_err(out, ref) < 1e-2, (kernel, schedule, H, S, d)
     np.testing.assert_allclose(out[:, 0], _np(v)[:, 0], atol=1e-2)
+
+
+@pytest.mark.parametrize("kernel", ["w1", "w64", "w64x4"])
+def test_flash_bf16_one_wave_per_simd_config(monkeypatch, kernel):
+    """8 x 2048 x 128 through each one-wavefront-per-SIMD kernel (balanced):
+    within 3e-3 of fp32 SDPA."""
+    from nkilab import ops, workloads
+
+    monkeypatch.setenv("NKL_FLASH_KERNEL", kernel)
+    monkeypatch.setenv("NKL_FLASH_SCHEDULE", "balanced")
+    q, k, v = (t.cuda() for t in workloads.attention_inputs())
+    out = _np(ops.attention(q, k, v))
+    assert rel_err(out, _sdpa_cpu(*(_np(t) for t in (q, k, v)))) <= 3e-3
 
 
 @pytest.mark.parametrize("qb,schedule", SCHEDULES)

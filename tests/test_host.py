@@ -59,13 +59,13 @@ def test_flash_scratch_sizes():
     """Balanced (split-block) scratch except for the largest shapes, where one
     workgroup per block needs none: 8 x 2048 has 17 units (128 queries x 32
     keys) per CU, 32 x 16384 has 4128 (the sizes assume a 256-CU device, which
-    is what the library assumes with no GPU).  One arrival counter per query
-    block: 128-query blocks at 8 x 2048, 64-query blocks at 1 x 4096."""
+    is what the library assumes with no GPU).  One arrival counter per
+    64-query block (the smallest block of any kernel), whatever the head dim."""
     from nkilab import _lib
 
     L = _lib.lib()
     assert L.nkl_flash_attn_causal_workspace_bytes(8, 2048, 128, 1) > 0
-    assert L.nkl_flash_attn_causal_counter_bytes(8, 2048, 1) == 8 * 16 * 4
+    assert L.nkl_flash_attn_causal_counter_bytes(8, 2048, 1) == 8 * 32 * 4
     assert L.nkl_flash_attn_causal_counter_bytes(1, 4096, 1) == 64 * 4
     assert L.nkl_flash_attn_causal_workspace_bytes(32, 16384, 128, 1) == 0
     assert L.nkl_flash_attn_causal_counter_bytes(32, 16384, 1) == 0
