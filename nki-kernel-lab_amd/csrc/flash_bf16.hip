@@ -83,7 +83,8 @@ struct Layout {
   static constexpr int SLOT = 64 * 4 * (NCO + 1);          // floats of one wavefront's state
   static constexpr int PART = WPT * SLOT;                  // floats of one partial block state
   static constexpr int XBYTES = NT * WPT * SLOT * 4;       // team hand-over area (reuses the stages)
-  static constexpr int SMEM = TOTAL * 2 > XBYTES ? TOTAL : XBYTES / 2;  // bf16 elements of LDS
+  // bf16 elements of LDS (a single team hands nothing over)
+  static constexpr int SMEM = NT == 1 || TOTAL * 2 > XBYTES ? TOTAL : XBYTES / 2;
 };
 
 struct Work {
@@ -134,7 +135,10 @@ __device__ __forceinline__ int range_of(long u, const Work& w) {
 }  // namespace
 
 template <int D, int WPT, int NT>
-__global__ __launch_bounds__(64 * WPT * NT) void flash_bf16_kernel(AttnArgs p, Work w) {
+// Two wavefronts per SIMD (at most 256 registers each): a 4-wavefront
+// workgroup then shares its CU with a second one.
+__global__ __launch_bounds__(64 * WPT * NT) __attribute__((amdgpu_waves_per_eu(2)))
+void flash_bf16_kernel(AttnArgs p, Work w) {
   using L = Layout<D, WPT, NT>;
   using MF = Mfma32<bf16>;
   constexpr int QB = L::QB, TT = L::TT;
@@ -387,7 +391,7 @@ __global__ __launch_bounds__(64 * WPT * NT) void flash_bf16_kernel(AttnArgs p, W
     const int own0 = team * OWN;
     const bool keeps = own0 < NDB;
     float l_tot = l_run + __shfl_xor(l_run, 32, kWave);  // lanes l and l ^ 32 hold the same query
-    {
+    if constexpr (NT > 1) {
       float4* xs = reinterpret_cast<float4*>(smem) + (team * WPT + wq) * (L::SLOT / 4) + lane;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
@@ -406,7 +410,7 @@ __global__ __launch_bounds__(64 * WPT * NT) void flash_bf16_kernel(AttnArgs p, W
       if (team == t && t * OWN < NDB)
 #pragma unroll
         for (int j = 0; j < OWN; ++j) own[j] = oacc[t * OWN + j < NDB ? t * OWN + j : NDB - 1];
-    __syncthreads();
+    if constexpr (NT > 1) __syncthreads();
 
     // Folds a state with max m2 and sum l2 into (m_run, l_tot) and returns the
     // weights of the running state (a1) and of the other (a2).  An empty state
@@ -420,27 +424,34 @@ __global__ __launch_bounds__(64 * WPT * NT) void flash_bf16_kernel(AttnArgs p, W
     };
     // Folds a wavefront state whose float4 chunk k (this lane's) is get(k);
     // all of its loads are issued before any is used.
+    // A 4-wavefront workgroup holds twice the staging registers per thread;
+    // it loads and folds one d-block at a time to stay within 256 registers.
+    constexpr int GJ = WPT * NT == 4 ? 1 : OWN;
     auto fold_state = [&](auto get) __attribute__((always_inline)) {
       const float4 st = get(L::NCO);
-      float4 v[OWN][4];
-      if (keeps) {
+      float a1 = 0.f, a2 = 0.f;
 #pragma unroll
-        for (int j = 0; j < OWN; ++j)
+      for (int j0 = 0; j0 < OWN; j0 += GJ) {
+        float4 v[GJ][4];
+        if (keeps) {
 #pragma unroll
-          for (int k = 0; k < 4; ++k) v[j][k] = get(4 * (own0 + j) + k);
-      }
-      float a1, a2;
-      weights(st.x, st.y, a1, a2);
-      if (keeps) {
+          for (int j = 0; j < GJ; ++j)
 #pragma unroll
-        for (int j = 0; j < OWN; ++j)
+            for (int k = 0; k < 4; ++k) v[j][k] = get(4 * (own0 + j0 + j) + k);
+        }
+        if (j0 == 0) weights(st.x, st.y, a1, a2);
+        if (keeps) {
 #pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            own[j][4 * k] = fmaf(v[j][k].x, a2, own[j][4 * k] * a1);
-            own[j][4 * k + 1] = fmaf(v[j][k].y, a2, own[j][4 * k + 1] * a1);
-            own[j][4 * k + 2] = fmaf(v[j][k].z, a2, own[j][4 * k + 2] * a1);
-            own[j][4 * k + 3] = fmaf(v[j][k].w, a2, own[j][4 * k + 3] * a1);
-          }
+          for (int j = 0; j < GJ; ++j)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              floatx16& o = own[j0 + j];
+              o[4 * k] = fmaf(v[j][k].x, a2, o[4 * k] * a1);
+              o[4 * k + 1] = fmaf(v[j][k].y, a2, o[4 * k + 1] * a1);
+              o[4 * k + 2] = fmaf(v[j][k].z, a2, o[4 * k + 2] * a1);
+              o[4 * k + 3] = fmaf(v[j][k].w, a2, o[4 * k + 3] * a1);
+            }
+        }
       }
     };
 #pragma unroll
@@ -451,28 +462,47 @@ __global__ __launch_bounds__(64 * WPT * NT) void flash_bf16_kernel(AttnArgs p, W
       }
 
     // Writes this team's d-blocks of O / l for the wavefront's 32 queries.
+    // The lane layout of O^T (lane: one query, 4-column groups of d) would
+    // make every 8-byte store touch a different row, so the wavefront stages
+    // its 32 x W block as bf16 rows in LDS and stores 16 bytes per lane, 8
+    // consecutive lanes per 128-byte row segment.  The staging area is the
+    // part of the wavefront's own hand-over slot that holds the d-blocks it
+    // keeps, which the hand-over neither writes nor reads (no barrier needed);
+    // a single team uses the idle stages.
     auto store_out = [&]() __attribute__((always_inline)) {
+      if (!keeps) return;
+      constexpr int W = 32 * OWN;     // d columns this team writes
+      constexpr int PITCH = W + 8;    // staging row pitch, elements
+      constexpr int CPRW = W / 8;     // 16-byte chunks per staged row
+      static_assert(NT > 1 || WPT * 32 * PITCH <= L::SMEM, "single-team staging fits the stages");
+      static_assert(NT == 1 || 32 * PITCH * 2 <= 4 * OWN * 1024, "staging fits the kept d-blocks of a slot");
+      bf16* stg = NT == 1 ? smem + wq * (32 * PITCH)
+                          : reinterpret_cast<bf16*>(reinterpret_cast<float4*>(smem) + (team * WPT + wq) * (L::SLOT / 4) +
+                                                    4 * own0 * 64);
       const float linv = 1.0f / l_tot;
-      if (keeps && myq < S) {
-        bf16* orow = static_cast<bf16*>(p.o) + (long)hh * p.o_sh + (long)myq * p.o_ss;
 #pragma unroll
-        for (int j = 0; j < OWN; ++j)
+      for (int j = 0; j < OWN; ++j)
 #pragma unroll
-          for (int bq = 0; bq < 4; ++bq) {
-            const int dd = 32 * (own0 + j) + 8 * bq + 4 * h32;
-            if (dd < dlim) {
-              float ov[4];
+        for (int bq = 0; bq < 4; ++bq) {
+          bf16x4 v4;
 #pragma unroll
-              for (int e = 0; e < 4; ++e) ov[e] = own[j][4 * bq + e] * linv;
-              store_vec<4>(orow + dd, ov);
-            }
-          }
+          for (int e = 0; e < 4; ++e) v4[e] = (bf16)(own[j][4 * bq + e] * linv);
+          *reinterpret_cast<bf16x4*>(stg + l32 * PITCH + 32 * j + 8 * bq + 4 * h32) = v4;
+        }
+      bf16* obase = static_cast<bf16*>(p.o) + (long)hh * p.o_sh + 32 * own0;
+#pragma unroll
+      for (int i = 0; i < 32 * CPRW / 64; ++i) {
+        const int cidx = lane + 64 * i, row = cidx / CPRW, cc = cidx % CPRW;
+        const uint4 x = *reinterpret_cast<const uint4*>(stg + row * PITCH + 8 * cc);
+        if (qw + row < S && 32 * own0 + 8 * cc < dlim)
+          *reinterpret_cast<uint4*>(obase + (long)(qw + row) * p.o_ss + 8 * cc) = x;
       }
     };
 
     // ---- the next segment of the range: its Q and first K/V tile are loaded
-    // once this segment's results are handed off, so that their latency
-    // overlaps the hand-off (and no release waits for them)
+    // before this segment's results are stored.  Loads and stores share the
+    // vector memory counter, so a load issued after the stores is held until
+    // the stores complete; issued first, their latencies overlap.
     const long next_u = bstart + t1;
     const bool more = next_u < u1;
     Seg nxt = cur;
@@ -491,9 +521,9 @@ __global__ __launch_bounds__(64 * WPT * NT) void flash_bf16_kernel(AttnArgs p, W
       vf = range_of(bstart, w);
       nparts = range_of(bstart + nt_b - 1, w) - vf + 1;
     }
+    prefetch();  // one definition of the next segment's registers for both paths (no copies, no wait)
     if (nparts == 1) {
       store_out();
-      prefetch();
     } else {
       // A partial state is PART floats: one wavefront state (layout above) per
       // wavefront; each workgroup has two slots, for the first and the last
@@ -523,7 +553,6 @@ __global__ __launch_bounds__(64 * WPT * NT) void flash_bf16_kernel(AttnArgs p, W
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
       if (tid == 0) arrival = atomicAdd(&w.count[hh * w.nqb + b], 1);
-      prefetch();
       __syncthreads();
       if (arrival == nparts - 1) {  // last to arrive: merge the others and write O
         // The others' states were complete before their arrivals, which
@@ -1101,14 +1130,16 @@ int cu_count() {
   return n;
 }
 
-// Kernels: teams of wavefronts sharing SIMDs, or one wavefront per SIMD with
-// 32 queries (4 per workgroup) or 64 queries (2 or 4 per workgroup).
-enum Kern { kTeams = 0, kW32x4 = 1, kW64x2 = 2, kW64x4 = 3 };
+// Kernels: teams of wavefronts sharing SIMDs (8 wavefronts per workgroup, or
+// 4 with two workgroups per CU), or one wavefront per SIMD with 32 queries (4
+// per workgroup) or 64 queries (2 or 4 per workgroup).
+enum Kern { kTeams = 0, kW32x4 = 1, kW64x2 = 2, kW64x4 = 3, kTeams4 = 4 };
 
 // A launch configuration: queries per block, a schedule and a kernel.  The
-// teams kernel takes 64-query blocks (2 wavefronts x 4 teams) or 128-query
-// blocks (4 wavefronts x 2 teams); the others take 32 or 64 queries per
-// wavefront times their wavefront count.
+// teams kernel takes 64-query blocks (2 wavefronts x 4 teams, or x 2 teams in
+// its 4-wavefront form) or 128-query blocks (4 wavefronts x 2 teams, or one
+// team); the others take 32 or 64 queries per wavefront times their
+// wavefront count.
 struct Config {
   int qb;
   int sched;
@@ -1116,7 +1147,7 @@ struct Config {
 };
 
 // Resident workgroups per CU: two for the two-wavefront kernel, else one.
-int wgs_per_cu(int kern) { return kern == kW64x2 ? 2 : 1; }
+int wgs_per_cu(int kern) { return kern == kW64x2 || kern == kTeams4 ? 2 : 1; }
 
 Work plan(int H, int S, Config cfg) {
   Work w{};
@@ -1168,11 +1199,12 @@ Config choose(int H, int S, int d) {
   }
   if (const char* f = getenv("NKL_FLASH_KERNEL")) {
     if (!strcmp(f, "teams")) cfg.kern = kTeams;
+    if (!strcmp(f, "teams4")) cfg.kern = kTeams4;
     if (!strcmp(f, "w1")) cfg.kern = kW32x4;
     if (!strcmp(f, "w64")) cfg.kern = kW64x2;
     if (!strcmp(f, "w64x4")) cfg.kern = kW64x4;
   }
-  if (d <= 64) cfg.kern = kTeams;
+  if (d <= 64 && cfg.kern != kTeams4) cfg.kern = kTeams;
   if (cfg.kern == kW32x4 || cfg.kern == kW64x2) cfg.qb = 128;
   if (cfg.kern == kW64x4) cfg.qb = 256;
   return cfg;
@@ -1201,11 +1233,17 @@ void launch_w(const AttnArgs& a, const Work& w, hipStream_t st) {
 }
 
 template <int D>
-void launch_qb(const AttnArgs& a, const Work& w, int qb, hipStream_t st) {
-  if (qb == 64)
+void launch_qb(const AttnArgs& a, const Work& w, int qb, int kern, hipStream_t st) {
+  if (kern == kTeams4) {
+    if (qb == 64)
+      launch<D, 2, 2>(a, w, st);
+    else
+      launch<D, 4, 1>(a, w, st);
+  } else if (qb == 64) {
     launch<D, 2, 4>(a, w, st);
-  else
+  } else {
     launch<D, 4, 2>(a, w, st);
+  }
 }
 
 }  // namespace
@@ -1241,7 +1279,7 @@ int flash_bf16_launch(const AttnArgs& a, void* workspace, size_t workspace_bytes
     w.part_bytes = (int)need;
     w.count = counters;
   }
-  if (cfg.kern != kTeams) {
+  if (cfg.kern == kW32x4 || cfg.kern == kW64x2 || cfg.kern == kW64x4) {
     if (cfg.kern == kW32x4)
       launch_w<1, 4>(a, w, st);
     else if (cfg.kern == kW64x2)
@@ -1251,11 +1289,11 @@ int flash_bf16_launch(const AttnArgs& a, void* workspace, size_t workspace_bytes
     return check_launch("nkl_flash_attn_causal");
   }
   if (a.d <= 32)
-    launch_qb<32>(a, w, cfg.qb, st);
+    launch_qb<32>(a, w, cfg.qb, cfg.kern, st);
   else if (a.d <= 64)
-    launch_qb<64>(a, w, cfg.qb, st);
+    launch_qb<64>(a, w, cfg.qb, cfg.kern, st);
   else
-    launch_qb<128>(a, w, cfg.qb, st);
+    launch_qb<128>(a, w, cfg.qb, cfg.kern, st);
   return check_launch("nkl_flash_attn_causal");
 }
 

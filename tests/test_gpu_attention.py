@@ -117,15 +117,18 @@ def test_flash_scratch_reused_across_shapes(rng):
 SCHEDULES = [(qb, s) for qb in ("64", "128") for s in ("balanced", "pairs", "block")]
 
 
+@pytest.mark.parametrize("kernel", ["teams", "teams4"])
 @pytest.mark.parametrize("qb,schedule", SCHEDULES)
 @pytest.mark.parametrize("H,S,d", [(1, 1, 64), (2, 65, 32), (3, 77, 128), (1, 300, 128), (4, 1000, 64),
                                    (2, 1537, 128), (5, 640, 96), (1, 129, 128), (1, 192, 128)])
-def test_flash_bf16_schedules(rng, monkeypatch, qb, schedule, H, S, d):
-    """Every configuration of the bf16 kernel -- 64- or 128-query blocks; split
-    blocks merged by the last workgroup, one workgroup per pair of blocks, or
-    one per block -- on ragged S and several head dims."""
+def test_flash_bf16_schedules(rng, monkeypatch, kernel, qb, schedule, H, S, d):
+    """Every configuration of the bf16 teams kernel -- 8 or 4 wavefronts; 64-
+    or 128-query blocks; split blocks merged by the last workgroup, one
+    workgroup per pair of blocks, or one per block -- on ragged S and several
+    head dims."""
     from nkilab import ops
 
+    monkeypatch.setenv("NKL_FLASH_KERNEL", kernel)
     monkeypatch.setenv("NKL_FLASH_SCHEDULE", schedule)
     monkeypatch.setenv("NKL_FLASH_QB", qb)
     q, k, v = (_bf(rng.standard_normal((H, S, d))) for _ in range(3))
@@ -153,7 +156,7 @@ def test_flash_bf16_one_wave_per_simd_kernel(rng, monkeypatch, kernel, schedule,
     np.testing.assert_allclose(out[:, 0], _np(v)[:, 0], atol=1e-2)
 
 
-@pytest.mark.parametrize("kernel", ["w1", "w64", "w64x4"])
+@pytest.mark.parametrize("kernel", ["w1", "w64", "w64x4", "teams4"])
 def test_flash_bf16_one_wave_per_simd_config(monkeypatch, kernel):
     """8 x 2048 x 128 through each one-wavefront-per-SIMD kernel (balanced):
     within 3e-3 of fp32 SDPA."""
