@@ -72,6 +72,25 @@ int nkl_gemm(const void* A, const void* B, void* C, const void* R,
              void* stream);
 
 /*
+ * C = silu(A . Wg^T) * (A . Wu^T): the decoder's gate and up projections and
+ * the SwiGLU between them in one GEMM (the fusion docs/STUDY_GUIDE.md:57
+ * suggests for nkilab/model.py:88, which calls ops.swiglu, nkilab/ops.py:64,
+ * on two matmul outputs).
+ *   A:   [M, K] bf16 (lda >= K).
+ *   Bgu: [2N, K] bf16 (ldb >= K), the rows of Wg and Wu ([N, K] each)
+ *        interleaved in groups of 32: rows 64 j .. 64 j + 31 are Wg rows
+ *        32 j .., rows 64 j + 32 .. 64 j + 63 are Wu rows 32 j ...
+ *   C:   [M, N] bf16 (ldc >= N).
+ * N must be a multiple of 32; pointers 16-byte aligned; K, lda, ldb, ldc
+ * multiples of 8.  The gate and up accumulators are rounded to bf16 before
+ * silu(gate) * up is formed in fp32 and rounded once, so C equals what two
+ * bf16 GEMMs followed by nkl_swiglu produce.
+ */
+int nkl_gemm_swiglu(const void* A, const void* Bgu, void* C, int M, int N,
+                    int K, long lda, long ldb, long ldc, int dtype,
+                    void* stream);
+
+/*
  * The reference's PSUM block check (nkilab/kernels/matmul.py:58): returns
  * NKL_OK when a BM x BN block of fp32 accumulator tiles fits the 8-tile
  * budget, NKL_ELIMIT (with a message naming PSUM) otherwise.  Used by the

@@ -189,6 +189,11 @@ __device__ __forceinline__ uint4 ld16_or_zero(const T* base, long off, bool ok) 
 }
 
 // Load KPER consecutive elements as one MFMA operand fragment.
+// silu(g) = g / (1 + e^-g) in fp32 (nkilab/kernels/norm.py:121-136).
+__device__ __forceinline__ float silu(float g) {
+  return g * __builtin_amdgcn_rcpf(1.0f + fast_exp2(-g * kLog2e));
+}
+
 __device__ __forceinline__ bf16x8 load_frag(const bf16* p) {
   return *reinterpret_cast<const bf16x8*>(p);
 }

@@ -20,6 +20,13 @@
 
 namespace nkl {
 
+// Epilogues of the LDS-DMA kernel.
+enum Epi {
+  kEpiElem = 0,    // one element per lane per store (any alignment)
+  kEpiStaged = 1,  // tile staged in LDS, 16 bytes per lane per store
+  kEpiSwiglu = 2,  // staged; adjacent 32-column tiles are gate and up: C = silu(gate) * up, N / 2 columns
+};
+
 struct GemmArgs {
   const void* A;
   const void* B;
@@ -28,6 +35,7 @@ struct GemmArgs {
   int M, N, K;
   long lda, ldb, ldc, ldr;
   long sA, sB, sC, sR;
+  int epi;  // Epi (the LDS-DMA kernel; the other kernels store elements)
 };
 
 template <typename T>
@@ -442,6 +450,73 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(GemmArgs p) {
 
   // Epilogue: accumulator element e of tile (i, j) is C[row][col] with
   // row = 8 * (e / 4) + 4 * (lane / 32) + e % 4, col = lane % 32.
+  if (p.epi != kEpiElem) {
+    // Staged: the wavefront writes its WM x WC block (fp32) to LDS rows, then
+    // each lane reads OE consecutive values of a row, adds the residual in
+    // fp32 and stores them as one 16-byte vector.  With the SwiGLU pairing,
+    // tiles 2k and 2k+1 of the wavefront hold gate and up for the same 32
+    // output columns (the weight rows are interleaved in groups of 32), and
+    // the block written is silu(bf16(gate)) * bf16(up): the values a gate and
+    // an up GEMM with bf16 outputs would hand the SwiGLU kernel.
+    constexpr int OE = 16 / sizeof(TO);  // output elements per 16-byte store
+    constexpr int WC_MAX = WN;           // staged columns per wavefront (SwiGLU: WN / 2)
+    constexpr int PITCH = WC_MAX + 4;    // staged row pitch, floats
+    static_assert(4 * WM * PITCH * 4 <= NS * STAGE, "the staged tile fits the stages");
+    __syncthreads();  // every wavefront is done with the stages
+    float* stg = reinterpret_cast<float*>(lds) + wid * (WM * PITCH);
+    const bool sw = p.epi == kEpiSwiglu;
+    const int wc = sw ? WN / 2 : WN;
+    if (sw) {
+      static_assert(TN % 2 == 0 || TN == 1, "gate/up tiles come in pairs");
+      if constexpr (TN % 2 == 0) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int k = 0; k < TN / 2; ++k)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const float g = to_f32<bf16>((bf16)acc[i][2 * k][e]);
+              const float u = to_f32<bf16>((bf16)acc[i][2 * k + 1][e]);
+              stg[(i * 32 + 8 * (e / 4) + 4 * lg + (e % 4)) * PITCH + k * 32 + lr] = silu(g) * u;
+            }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) stg[(i * 32 + 8 * (e / 4) + 4 * lg + (e % 4)) * PITCH + j * 32 + lr] = acc[i][j][e];
+    }
+    // Rows of the block go to rows m0 + wm WM ..; columns to c0 ...
+    const int c0 = sw ? (n0 + wn * WN) / 2 : n0 + wn * WN;
+    const int ncols = sw ? p.N / 2 : p.N;
+    const int cpr = wc / OE;  // 16-byte chunks per staged row
+#pragma unroll 4
+    for (int c = lane; c < WM * cpr; c += 64) {
+      const int rl = c / cpr, cl = (c % cpr) * OE;
+      const int row = m0 + wm * WM + rl, col = c0 + cl;
+      if (row < p.M && col < ncols) {
+        float v[OE];
+#pragma unroll
+        for (int e = 0; e < OE; e += 4) {
+          const float4 x = *reinterpret_cast<const float4*>(stg + rl * PITCH + cl + e);
+          v[e] = x.x;
+          v[e + 1] = x.y;
+          v[e + 2] = x.z;
+          v[e + 3] = x.w;
+        }
+        if (R) {
+          float r[OE];
+          load16(R + (long)row * p.ldr + col, r);
+#pragma unroll
+          for (int e = 0; e < OE; ++e) v[e] += r[e];
+        }
+        store_vec<OE>(C + (long)row * p.ldc + col, v);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -462,6 +537,16 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(GemmArgs p) {
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// The staged epilogue stores 16-byte vectors: C (and R) rows, batch strides
+// and N must keep every vector 16-byte aligned.
+template <typename TO>
+static bool staged_ok(const GemmArgs& a) {
+  constexpr long OE = 16 / sizeof(TO);
+  const bool c_ok = aligned16(a.C) && a.ldc % OE == 0 && a.sC % OE == 0 && a.N % OE == 0;
+  const bool r_ok = !a.R || (aligned16(a.R) && a.ldr % OE == 0 && a.sR % OE == 0);
+  return c_ok && r_ok;
+}
+
 template <typename T, typename TO, bool BT>
 static int gemm_dispatch(const GemmArgs& a, int batch, int variant, hipStream_t st) {
   constexpr int E = VecE<T>::value;
@@ -480,15 +565,17 @@ static int gemm_dispatch(const GemmArgs& a, int batch, int variant, hipStream_t 
     const long a_bytes = 2L * ((long)(a.M - 1) * a.lda + a.K), b_bytes = BT ? 2L * ((long)(a.N - 1) * a.ldb + a.K)
                                                                         : 2L * ((long)(a.K - 1) * a.ldb + a.N);
     if (a_bytes < (1L << 31) && b_bytes < (1L << 31)) {
+      GemmArgs g = a;
+      g.epi = staged_ok<TO>(a) ? kEpiStaged : kEpiElem;
       if (t128 >= 256) {
         const long tiles = (long)((a.M + 127) / 128) * ((a.N + 127) / 128);
-        gemm_dma_kernel<TO, 128, 128, BT, 4><<<dim3((unsigned)tiles, 1, batch), dim3(256), 0, st>>>(a);
+        gemm_dma_kernel<TO, 128, 128, BT, 4><<<dim3((unsigned)tiles, 1, batch), dim3(256), 0, st>>>(g);
       } else if (t64x128 >= 256) {
         const long tiles = (long)((a.M + 63) / 64) * ((a.N + 127) / 128);
-        gemm_dma_kernel<TO, 64, 128, BT, 6><<<dim3((unsigned)tiles, 1, batch), dim3(256), 0, st>>>(a);
+        gemm_dma_kernel<TO, 64, 128, BT, 6><<<dim3((unsigned)tiles, 1, batch), dim3(256), 0, st>>>(g);
       } else {
         const long tiles = (long)((a.M + 63) / 64) * ((a.N + 63) / 64);
-        gemm_dma_kernel<TO, 64, 64, BT, 8><<<dim3((unsigned)tiles, 1, batch), dim3(256), 0, st>>>(a);
+        gemm_dma_kernel<TO, 64, 64, BT, 8><<<dim3((unsigned)tiles, 1, batch), dim3(256), 0, st>>>(g);
       }
       return check_launch("nkl_gemm(blocked)");
     }
@@ -533,6 +620,37 @@ extern "C" int nkl_gemm(const void* A, const void* B, void* C, const void* R, in
   if (dtype_in == NKL_BF16 && dtype_out == NKL_BF16) return gemm_layout<bf16, bf16>(a, b_trans, batch, variant, st);
   if (dtype_in == NKL_BF16 && dtype_out == NKL_F32) return gemm_layout<bf16, float>(a, b_trans, batch, variant, st);
   return set_error(NKL_EDTYPE, "nkl_gemm: unsupported dtype pair (%d -> %d)", dtype_in, dtype_out);
+}
+
+extern "C" int nkl_gemm_swiglu(const void* A, const void* Bgu, void* C, int M, int N, int K, long lda, long ldb,
+                               long ldc, int dtype, void* stream) {
+  if (M < 0 || N < 0 || K < 0)
+    return set_error(NKL_EINVAL, "nkl_gemm_swiglu: negative shape M=%d N=%d K=%d", M, N, K);
+  if (dtype != NKL_BF16) return set_error(NKL_EDTYPE, "nkl_gemm_swiglu: only bf16 is supported (dtype %d)", dtype);
+  if (M == 0 || N == 0) return NKL_OK;
+  if (N % 32 != 0) return set_error(NKL_EINVAL, "nkl_gemm_swiglu: N=%d must be a multiple of 32", N);
+  if (!A || !Bgu || !C) return set_error(NKL_EINVAL, "nkl_gemm_swiglu: null operand pointer");
+  if (lda < K || ldb < K || ldc < N)
+    return set_error(NKL_EINVAL, "nkl_gemm_swiglu: leading dimension too small (lda=%ld ldb=%ld ldc=%ld)", lda, ldb,
+                     ldc);
+  if (!aligned16(A) || !aligned16(Bgu) || !aligned16(C) || K % 8 != 0 || lda % 8 != 0 || ldb % 8 != 0 ||
+      ldc % 8 != 0)
+    return set_error(NKL_EINVAL, "nkl_gemm_swiglu: operands must be 16-byte aligned with K and leading dimensions "
+                     "multiples of 8");
+  const long a_bytes = 2L * ((long)(M - 1) * lda + K), b_bytes = 2L * ((long)(2L * N - 1) * ldb + K);
+  if (a_bytes >= (1L << 31) || b_bytes >= (1L << 31))
+    return set_error(NKL_EINVAL, "nkl_gemm_swiglu: operands must be under 2 GiB");
+  GemmArgs a{A, Bgu, C, nullptr, M, 2 * N, K, lda, ldb, ldc, 0, 0, 0, 0, 0, kEpiSwiglu};
+  hipStream_t st = (hipStream_t)stream;
+  // Tiles 128 columns wide: each wavefront's 64 columns are one gate/up pair.
+  const long t128 = (long)((M + 127) / 128) * ((2L * N + 127) / 128);
+  if (t128 >= 256) {
+    gemm_dma_kernel<bf16, 128, 128, true, 4><<<dim3((unsigned)t128), dim3(256), 0, st>>>(a);
+  } else {
+    const long tiles = (long)((M + 63) / 64) * ((2L * N + 127) / 128);
+    gemm_dma_kernel<bf16, 64, 128, true, 6><<<dim3((unsigned)tiles), dim3(256), 0, st>>>(a);
+  }
+  return check_launch("nkl_gemm_swiglu");
 }
 
 extern "C" int nkl_check_blocks(int BM, int BN) {

@@ -204,10 +204,8 @@ __global__ __launch_bounds__(256) void rmsnorm_loop_kernel(const TI* __restrict_
 }
 
 // -------------------------------------------------------------- SwiGLU --
-// nkilab/kernels/norm.py:121-136: a = silu(g) in fp32; y = a * u rounded once.
-__device__ __forceinline__ float silu(float g) {
-  return g * __builtin_amdgcn_rcpf(1.0f + fast_exp2(-g * kLog2e));
-}
+// nkilab/kernels/norm.py:121-136: a = silu(g) in fp32; y = a * u rounded once
+// (silu is in common.h, shared with the GEMM's gate/up epilogue).
 
 // Each thread handles UNROLL 16-byte vectors spaced a grid-width apart.
 template <typename T, int UNROLL>

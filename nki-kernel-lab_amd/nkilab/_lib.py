@@ -24,6 +24,7 @@ SIGNATURES = {
     "nkl_last_error_string": (ctypes.c_char_p, []),
     "nkl_gemm": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_long, _c_long, _c_long, _c_long,
                           _c_int, _c_int, _c_long, _c_long, _c_long, _c_long, _c_int, _c_int, _c_int, _vp]),
+    "nkl_gemm_swiglu": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_long, _c_long, _c_long, _c_int, _vp]),
     "nkl_check_blocks": (_c_int, [_c_int, _c_int]),
     "nkl_softmax": (_c_int, [_vp, _vp, _c_int, _c_int, _c_long, _c_long, _c_int, _vp]),
     "nkl_softmax_unfused_workspace_bytes": (_c_size, [_c_int, _c_int]),

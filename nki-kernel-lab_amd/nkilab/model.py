@@ -18,6 +18,9 @@ Differences from the reference's host glue, none of which changes the math:
     not copies (model.py:84-86);
   * the residual adds run in the out-projection / down-projection GEMM
     epilogues (model.py:86, :89);
+  * in bf16 the gate and up projections and the SwiGLU between them
+    (model.py:88) are one GEMM over the two weights interleaved in groups of
+    32 rows, with SwiGLU in its epilogue (the same values as the three calls);
   * ``compute_dtype="bfloat16"`` runs the block in bf16 with an fp32 residual
     stream (the GEMMs that feed the residual emit fp32).  The default keeps
     the reference's behaviour: everything in x's dtype.
@@ -106,6 +109,21 @@ def _device_param(block: nn.Module, name: str, p: torch.Tensor, dtype: torch.dty
     return t
 
 
+def _packed_gate_up(block: DecoderBlock, dev: torch.device) -> torch.Tensor:
+    """pack_gate_up(Wg, Wu) in bf16 on dev, rebuilt when either weight changes."""
+    cache = block.__dict__.setdefault("_nkl_param_cache", {})
+    key = ("gate_up", torch.bfloat16, dev)
+    stamp = tuple((p.data_ptr(), p._version) for p in (block.wg.weight, block.wu.weight))
+    hit = cache.get(key)
+    if hit is not None and hit[0] == stamp:
+        return hit[1]
+    wg = block.wg.weight.detach().to(device=dev, dtype=torch.bfloat16)
+    wu = block.wu.weight.detach().to(device=dev, dtype=torch.bfloat16)
+    t = ops.pack_gate_up(wg, wu)
+    cache[key] = (stamp, t)
+    return t
+
+
 def nki_forward(block: DecoderBlock, x, attention_variant: str = "flash_pipelined", compute_dtype=None):
     """The same block with every heavy op on the HIP kernels (model.py:70-89).
 
@@ -138,12 +156,16 @@ def nki_forward(block: DecoderBlock, x, attention_variant: str = "flash_pipeline
     ops.linear_into(a, W["wo"], x1, residual=xt)
     h2 = torch.empty((S, d), dtype=cdt, device=dev)
     ops.rmsnorm_into(x1, g2, h2, cfg.eps)
-    gate = torch.empty((S, cfg.d_ff), dtype=cdt, device=dev)
-    up = torch.empty((S, cfg.d_ff), dtype=cdt, device=dev)
-    ops.linear_into(h2, W["wg"], gate)
-    ops.linear_into(h2, W["wu"], up)
     act = torch.empty((S, cfg.d_ff), dtype=cdt, device=dev)
-    ops.swiglu_into(gate, up, act)
+    if cdt == torch.bfloat16 and cfg.d_ff % ops.GATE_UP_GROUP == 0 and d % 8 == 0:
+        # gate, up and SwiGLU in one GEMM over the packed weight (same values)
+        ops.gemm_swiglu_into(h2, _packed_gate_up(block, dev), act)
+    else:
+        gate = torch.empty((S, cfg.d_ff), dtype=cdt, device=dev)
+        up = torch.empty((S, cfg.d_ff), dtype=cdt, device=dev)
+        ops.linear_into(h2, W["wg"], gate)
+        ops.linear_into(h2, W["wu"], up)
+        ops.swiglu_into(gate, up, act)
     out = torch.empty((S, d), dtype=rdt, device=dev)
     ops.linear_into(act, W["wd"], out, residual=x1)
     return from_device(out, kind)

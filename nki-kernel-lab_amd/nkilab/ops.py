@@ -104,6 +104,42 @@ def linear_into(a: torch.Tensor, w: torch.Tensor, c: torch.Tensor, residual: tor
     return _gemm(a, wm, ldw, True, c, residual, variant)
 
 
+GATE_UP_GROUP = 32  # rows of Wg, then of Wu, per group of the packed gate/up weight
+
+
+def pack_gate_up(wg: torch.Tensor, wu: torch.Tensor) -> torch.Tensor:
+    """The [2N, K] weight ``gemm_swiglu_into`` takes: the rows of Wg and Wu
+    ([N, K] each, nn.Linear layout) interleaved in groups of 32."""
+    if wg.shape != wu.shape or wg.dim() != 2:
+        raise ValueError(f"pack_gate_up: Wg {tuple(wg.shape)} and Wu {tuple(wu.shape)} must be equal 2-D shapes")
+    N, K = wg.shape
+    if N % GATE_UP_GROUP:
+        raise ValueError(f"pack_gate_up: N={N} must be a multiple of {GATE_UP_GROUP}")
+    g = wg.reshape(N // GATE_UP_GROUP, GATE_UP_GROUP, K)
+    u = wu.reshape(N // GATE_UP_GROUP, GATE_UP_GROUP, K)
+    return torch.stack((g, u), dim=1).reshape(2 * N, K).contiguous()
+
+
+def gemm_swiglu_into(a: torch.Tensor, w_gu: torch.Tensor, c: torch.Tensor) -> torch.Tensor:
+    """c = silu(a @ Wg^T) * (a @ Wu^T) in one GEMM (model.py:88's gate, up and
+    SwiGLU), for bf16 a [M, K], the packed weight w_gu = pack_gate_up(Wg, Wu)
+    [2N, K] and c [M, N].  Equal to two bf16 linear_into calls and swiglu_into."""
+    M, K = a.shape
+    N = c.shape[1]
+    if w_gu.shape != (2 * N, K):
+        raise ValueError(f"gemm_swiglu_into: packed weight {tuple(w_gu.shape)} does not match [2*{N}, {K}]")
+    if not (a.dtype == w_gu.dtype == c.dtype == torch.bfloat16):
+        raise TypeError("gemm_swiglu_into: bf16 operands only")
+    a, lda = _row_major(a, K)
+    wm, ldw = _row_major(w_gu, K)
+    if c.dim() != 2 or (c.stride(1) != 1 and N > 1) or (M > 1 and c.stride(0) < N):
+        raise ValueError("gemm_swiglu_into: the output must be a row-major [M, N] tensor")
+    ldc = c.stride(0) if M > 1 else max(N, 1)
+    _lib.call("nkl_gemm_swiglu", ptr(a), ptr(wm), ptr(c), M, N, K, lda, ldw, ldc, dtype_code(a.dtype),
+              stream_handle())
+    return c
+
+
 def matmul(a, b, variant: str = "blocked"):
     """C = A @ B for any shapes (ops.py:38-52).  bf16 inputs accumulate in fp32 and
     C is rounded once; the output dtype is the input dtype."""

@@ -116,3 +116,57 @@ def test_nonaligned_leading_dimensions(rng):
     c = ops.matmul(a, b)
     ref = _np(a).astype(np.float64) @ _np(b)
     assert rel_err(_np(c), ref) < 1e-5
+
+
+@pytest.mark.parametrize("M,K,N,out_dt,res", [(192, 320, 256, torch.bfloat16, False), (130, 64, 72, torch.bfloat16, True),
+                                               (257, 128, 40, torch.float32, True), (1000, 256, 1536, torch.float32, True),
+                                               (64, 96, 132, torch.float32, False)])
+def test_staged_epilogue_matches_element_epilogue(rng, M, K, N, out_dt, res):
+    """bf16 GEMMs whose outputs take the 16-byte staged epilogue (aligned rows)
+    against the same product written into a view whose rows are not 16-byte
+    aligned (the element epilogue): identical values, residual included."""
+    from nkilab import ops
+
+    a = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).to(torch.bfloat16).cuda()
+    w = torch.from_numpy(rng.standard_normal((N, K)).astype(np.float32)).to(torch.bfloat16).cuda()
+    r = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float32)).to(out_dt).cuda() if res else None
+    c = torch.empty((M, N), dtype=out_dt, device="cuda")
+    ops.linear_into(a, w, c, residual=r)
+    big = torch.empty((M, N + 1), dtype=out_dt, device="cuda")
+    c_odd = big[:, 1:]  # data pointer off by one element, ld N + 1
+    ops.linear_into(a, w, c_odd, residual=r)
+    assert torch.equal(c, c_odd)
+    ref = _np(a).astype(np.float64) @ _np(w).astype(np.float64).T + (_np(r) if res else 0)
+    assert rel_err(_np(c), ref) < (1e-5 if out_dt == torch.float32 else 1e-2)
+
+
+@pytest.mark.parametrize("M,K,N", [(2048, 2048, 5632), (300, 256, 96), (64, 128, 32), (1, 64, 64), (513, 384, 704)])
+def test_gemm_swiglu_equals_gate_up_then_swiglu(rng, M, K, N):
+    """The fused gate/up GEMM with SwiGLU in its epilogue is bit-identical to
+    two bf16 linear layers followed by the SwiGLU kernel (model.py:88), and
+    within bf16 tolerance of the float64 product."""
+    from nkilab import ops
+
+    h = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).to(torch.bfloat16).cuda()
+    wg = torch.from_numpy((0.05 * rng.standard_normal((N, K))).astype(np.float32)).to(torch.bfloat16).cuda()
+    wu = torch.from_numpy((0.05 * rng.standard_normal((N, K))).astype(np.float32)).to(torch.bfloat16).cuda()
+    fused = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    ops.gemm_swiglu_into(h, ops.pack_gate_up(wg, wu), fused)
+    gate, up, act = (torch.empty((M, N), dtype=torch.bfloat16, device="cuda") for _ in range(3))
+    ops.linear_into(h, wg, gate)
+    ops.linear_into(h, wu, up)
+    ops.swiglu_into(gate, up, act)
+    assert torch.equal(fused, act)
+    g64 = _np(h).astype(np.float64) @ _np(wg).astype(np.float64).T
+    u64 = _np(h).astype(np.float64) @ _np(wu).astype(np.float64).T
+    ref = g64 / (1 + np.exp(-g64)) * u64
+    assert rel_err(_np(fused), ref) < 2e-2
+
+
+def test_gemm_swiglu_rejects_bad_shapes():
+    from nkilab import ops
+
+    h = torch.zeros((16, 64), dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros((2 * 48, 64), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError, match="multiple of 32"):
+        ops.gemm_swiglu_into(h, w, torch.empty((16, 48), dtype=torch.bfloat16, device="cuda"))

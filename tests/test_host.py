@@ -73,6 +73,35 @@ def test_flash_scratch_sizes():
     assert L.nkl_flash_attn_causal_workspace_bytes(0, 2048, 128, 1) == 0
 
 
+def test_pack_gate_up_interleaves_groups_of_32():
+    """Rows 64 j .. 64 j + 31 of the packed weight are Wg's rows 32 j .., the
+    next 32 are Wu's, as nkl_gemm_swiglu expects."""
+    import torch
+
+    from nkilab import ops
+
+    N, K = 96, 5
+    wg = torch.arange(N * K, dtype=torch.float32).reshape(N, K)
+    wu = -wg - 1
+    p = ops.pack_gate_up(wg, wu)
+    assert p.shape == (2 * N, K)
+    for j in range(N // 32):
+        assert torch.equal(p[64 * j:64 * j + 32], wg[32 * j:32 * j + 32])
+        assert torch.equal(p[64 * j + 32:64 * j + 64], wu[32 * j:32 * j + 32])
+    with pytest.raises(ValueError):
+        ops.pack_gate_up(wg[:40], wu[:40])
+
+
+def test_gemm_swiglu_abi_checks():
+    from nkilab import _lib
+
+    L = _lib.lib()
+    assert L.nkl_gemm_swiglu(None, None, None, 4, 48, 64, 64, 64, 48, 1, None) == -1  # N % 32
+    assert b"multiple of 32" in L.nkl_last_error_string()
+    assert L.nkl_gemm_swiglu(None, None, None, 4, 64, 64, 64, 64, 64, 0, None) == -2  # fp32
+    assert L.nkl_gemm_swiglu(None, None, None, 0, 64, 64, 64, 64, 64, 1, None) == 0   # empty
+
+
 def test_psum_block_check():
     from nkilab import _lib
 
