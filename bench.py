@@ -166,7 +166,7 @@ def bench_decoder(reps, warmup):
     flops = 227_641_655_296
     return {"us": sec * 1e6, "tflops": flops / sec / 1e12, "frac": flops / sec / 1e12 / PEAK_BF16_TFLOPS,
             "eager_us": eager * 1e6,
-            "note": "8 launches per block (gate, up and SwiGLU fused in bf16) replayed from a HIP graph; eager_us is the Python loop's wall clock"}
+            "note": "7 launches per block (2 RMSNorm, QKV, attention, out-proj, fused gate/up/SwiGLU, down-proj) replayed from a HIP graph; eager_us is the Python loop's wall clock"}
 
 
 # ---------------------------------------------------------- CPU baseline --
