@@ -192,6 +192,40 @@ int nkl_attention_naive(const void* q, const void* k, const void* v, void* o,
                         long v_sh, long v_ss, long o_sh, long o_ss,
                         float scale, int dtype, void* stream);
 
+/*
+ * Grouped-query (and multi-query) forms of the two entry points above: q and
+ * o have H heads, k and v have Hkv heads (H a multiple of Hkv), and query
+ * head h attends with K/V head h / (H / Hkv).  No counterpart in the
+ * reference, whose README lists GQA/MQA among the features it does not
+ * implement (README.md:89); with Hkv == H they equal nkl_flash_attn_causal_ws
+ * and nkl_attention_naive.  Scratch sizes are those of the H-head call.
+ */
+int nkl_flash_attn_causal_gqa(const void* q, const void* k, const void* v,
+                              void* o, void* workspace, size_t workspace_bytes,
+                              int* counters, size_t counter_bytes, int H,
+                              int Hkv, int S, int d, long q_sh, long q_ss,
+                              long k_sh, long k_ss, long v_sh, long v_ss,
+                              long o_sh, long o_ss, float scale, int dtype,
+                              void* stream);
+int nkl_attention_naive_gqa(const void* q, const void* k, const void* v,
+                            void* o, void* workspace, size_t workspace_bytes,
+                            int H, int Hkv, int S, int d, long q_sh, long q_ss,
+                            long k_sh, long k_ss, long v_sh, long v_ss,
+                            long o_sh, long o_ss, float scale, int dtype,
+                            void* stream);
+
+/*
+ * Rotary position embedding, rotate-half layout (RoFormer, as GPT-NeoX and
+ * Llama apply it): for each head h and row s of x [H, S, d] (strides x_sh,
+ * x_ss; d even), element i < d/2 and element i + d/2 rotate by the angle
+ * (pos0 + s) * base^(-2 i / d).  fp32 arithmetic, one rounding per output;
+ * y may be x (in place).  No counterpart in the reference (README.md:89 lists
+ * rotary embeddings as not implemented); applied to q and k before attention.
+ */
+int nkl_rope(const void* x, void* y, int H, int S, int d, long x_sh, long x_ss,
+             long y_sh, long y_ss, int pos0, float base, int dtype,
+             void* stream);
+
 #ifdef __cplusplus
 }
 #endif

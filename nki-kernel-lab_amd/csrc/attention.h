@@ -12,7 +12,8 @@ struct AttnArgs {
   void* o;
   int H, S, d;
   long q_sh, q_ss, k_sh, k_ss, v_sh, v_ss, o_sh, o_ss;
-  float c;  // softmax scale * log2(e): p = exp2(s * c - m)
+  float c;    // softmax scale * log2(e): p = exp2(s * c - m)
+  int group;  // query heads per K/V head (grouped-query attention; 1 for multi-head)
 };
 
 // bf16 flash attention (flash_bf16.hip).  With a workspace of

@@ -79,8 +79,8 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(AttnArgs p) {
   const int myq = qw + r;       // this lane's query
 
   const T* Q = static_cast<const T*>(p.q) + (long)h * p.q_sh;
-  const T* K = static_cast<const T*>(p.k) + (long)h * p.k_sh;
-  const T* V = static_cast<const T*>(p.v) + (long)h * p.v_sh;
+  const T* K = static_cast<const T*>(p.k) + (long)(h / p.group) * p.k_sh;  // shared K/V head (GQA)
+  const T* V = static_cast<const T*>(p.v) + (long)(h / p.group) * p.v_sh;
   T* O = static_cast<T*>(p.o) + (long)h * p.o_sh;
 
   // Q^T fragments: lane (r, g) holds Q[myq][MK * f + KPER * g + j].
@@ -351,17 +351,32 @@ static int check_attn(const char* fn, const void* q, const void* k, const void* 
   return NKL_OK;
 }
 
+static int flash_entry(const char* fn, const void* q, const void* k, const void* v, void* o, void* workspace,
+                       size_t workspace_bytes, int* counters, size_t counter_bytes, bool ws_entry, int H, int Hkv,
+                       int S, int d, const long* st8, float scale, int dtype, void* stream) {
+  int rc = check_attn(fn, q, k, v, o, H, S, d, dtype, st8);
+  if (rc) return rc;
+  if (Hkv < 1 || H % Hkv != 0)
+    return set_error(NKL_EINVAL, "%s: H=%d query heads do not divide into Hkv=%d K/V heads", fn, H, Hkv);
+  if (H == 0 || S == 0) return NKL_OK;
+  AttnArgs a{q, k, v, o, H, S, d, st8[0], st8[1], st8[2], st8[3], st8[4], st8[5], st8[6], st8[7], scale * kLog2e,
+             H / Hkv};
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == NKL_BF16) {
+    if (!ws_entry) return flash_bf16_launch(a, nullptr, 0, nullptr, 0, st);
+    // Shapes that need no scratch (size 0) accept a null workspace.
+    if (!workspace && flash_bf16_workspace_bytes(H, S, d) > 0) return set_error(NKL_EWORKSPACE, "%s: null workspace", fn);
+    return flash_bf16_launch(a, workspace, workspace_bytes, counters, counter_bytes, st);
+  }
+  return flash_f32_dispatch(a, st);
+}
+
 extern "C" int nkl_flash_attn_causal(const void* q, const void* k, const void* v, void* o, int H, int S, int d,
                                      long q_sh, long q_ss, long k_sh, long k_ss, long v_sh, long v_ss, long o_sh,
                                      long o_ss, float scale, int dtype, void* stream) {
   const long strides[8] = {q_sh, q_ss, k_sh, k_ss, v_sh, v_ss, o_sh, o_ss};
-  int rc = check_attn("nkl_flash_attn_causal", q, k, v, o, H, S, d, dtype, strides);
-  if (rc) return rc;
-  if (H == 0 || S == 0) return NKL_OK;
-  AttnArgs a{q, k, v, o, H, S, d, q_sh, q_ss, k_sh, k_ss, v_sh, v_ss, o_sh, o_ss, scale * kLog2e};
-  hipStream_t st = (hipStream_t)stream;
-  if (dtype == NKL_BF16) return flash_bf16_launch(a, nullptr, 0, nullptr, 0, st);
-  return flash_f32_dispatch(a, st);
+  return flash_entry("nkl_flash_attn_causal", q, k, v, o, nullptr, 0, nullptr, 0, false, H, H > 0 ? H : 1, S, d,
+                     strides, scale, dtype, stream);
 }
 
 extern "C" size_t nkl_flash_attn_causal_workspace_bytes(int H, int S, int d, int dtype) {
@@ -379,18 +394,17 @@ extern "C" int nkl_flash_attn_causal_ws(const void* q, const void* k, const void
                                         int d, long q_sh, long q_ss, long k_sh, long k_ss, long v_sh, long v_ss,
                                         long o_sh, long o_ss, float scale, int dtype, void* stream) {
   const long strides[8] = {q_sh, q_ss, k_sh, k_ss, v_sh, v_ss, o_sh, o_ss};
-  int rc = check_attn("nkl_flash_attn_causal_ws", q, k, v, o, H, S, d, dtype, strides);
-  if (rc) return rc;
-  if (H == 0 || S == 0) return NKL_OK;
-  AttnArgs a{q, k, v, o, H, S, d, q_sh, q_ss, k_sh, k_ss, v_sh, v_ss, o_sh, o_ss, scale * kLog2e};
-  hipStream_t st = (hipStream_t)stream;
-  if (dtype == NKL_BF16) {
-    // Shapes that need no scratch (size 0) accept a null workspace.
-    if (!workspace && flash_bf16_workspace_bytes(H, S, d) > 0)
-      return set_error(NKL_EWORKSPACE, "nkl_flash_attn_causal_ws: null workspace");
-    return flash_bf16_launch(a, workspace, workspace_bytes, counters, counter_bytes, st);
-  }
-  return flash_f32_dispatch(a, st);
+  return flash_entry("nkl_flash_attn_causal_ws", q, k, v, o, workspace, workspace_bytes, counters, counter_bytes,
+                     true, H, H > 0 ? H : 1, S, d, strides, scale, dtype, stream);
+}
+
+extern "C" int nkl_flash_attn_causal_gqa(const void* q, const void* k, const void* v, void* o, void* workspace,
+                                         size_t workspace_bytes, int* counters, size_t counter_bytes, int H, int Hkv,
+                                         int S, int d, long q_sh, long q_ss, long k_sh, long k_ss, long v_sh,
+                                         long v_ss, long o_sh, long o_ss, float scale, int dtype, void* stream) {
+  const long strides[8] = {q_sh, q_ss, k_sh, k_ss, v_sh, v_ss, o_sh, o_ss};
+  return flash_entry("nkl_flash_attn_causal_gqa", q, k, v, o, workspace, workspace_bytes, counters, counter_bytes,
+                     true, H, Hkv, S, d, strides, scale, dtype, stream);
 }
 
 extern "C" size_t nkl_attention_naive_workspace_bytes(int H, int S, int dtype) {
@@ -400,36 +414,66 @@ extern "C" size_t nkl_attention_naive_workspace_bytes(int H, int S, int dtype) {
   return sc + n * (dtype == NKL_F32 ? 4 : 2);
 }
 
+static int naive_entry(const char* fn, const void* q, const void* k, const void* v, void* o, void* workspace,
+                       size_t workspace_bytes, int H, int Hkv, int S, int d, const long* st8, float scale, int dtype,
+                       void* stream) {
+  int rc = check_attn(fn, q, k, v, o, H, S, d, dtype, st8);
+  if (rc) return rc;
+  if (Hkv < 1 || H % Hkv != 0)
+    return set_error(NKL_EINVAL, "%s: H=%d query heads do not divide into Hkv=%d K/V heads", fn, H, Hkv);
+  if (H == 0 || S == 0) return NKL_OK;
+  const size_t need = nkl_attention_naive_workspace_bytes(H, S, dtype);
+  if (!workspace || workspace_bytes < need)
+    return set_error(NKL_EWORKSPACE, "%s: workspace of %zu bytes needed, %zu given", fn, need, workspace_bytes);
+  const long q_sh = st8[0], q_ss = st8[1], k_sh = st8[2], k_ss = st8[3], v_sh = st8[4], v_ss = st8[5],
+             o_sh = st8[6], o_ss = st8[7];
+  const size_t n = (size_t)H * S * S;
+  float* sc = static_cast<float*>(workspace);
+  char* pr = static_cast<char*>(workspace) + (n * 4 + 255) / 256 * 256;
+  const size_t esz = dtype == NKL_F32 ? 4 : 2;
+  hipStream_t st = (hipStream_t)stream;
+  const long SS = (long)S * S;
+  const int G = H / Hkv;
+  // Query head h = kvh * G + g uses K/V head kvh.  For each g, the heads
+  // g, G + g, ... form one batched GEMM over the K/V heads (batch strides
+  // G times the query / score / output strides).
+  // pass 1: scores[h] = Q[h] . K[h / G]^T (fp32)
+  for (int g = 0; g < G; ++g) {
+    rc = nkl_gemm(static_cast<const char*>(q) + g * q_sh * esz, k, sc + g * SS, nullptr, S, S, d, q_ss, k_ss, S, 0, 1,
+                  Hkv, G * q_sh, k_sh, G * SS, 0, dtype, NKL_F32, NKL_GEMM_BLOCKED, stream);
+    if (rc) return rc;
+  }
+  // pass 2: scale, mask, row softmax -> P
+  const dim3 grid((unsigned)(((long)H * S + 3) / 4)), block(256);
+  if (dtype == NKL_BF16)
+    masked_softmax_kernel<bf16><<<grid, block, 0, st>>>(sc, reinterpret_cast<bf16*>(pr), H, S, scale);
+  else
+    masked_softmax_kernel<float><<<grid, block, 0, st>>>(sc, reinterpret_cast<float*>(pr), H, S, scale);
+  rc = check_launch(fn);
+  if (rc) return rc;
+  // pass 3: O[h] = P[h] . V[h / G]
+  for (int g = 0; g < G; ++g) {
+    rc = nkl_gemm(pr + g * SS * esz, v, static_cast<char*>(o) + g * o_sh * esz, nullptr, S, d, S, S, v_ss, o_ss, 0,
+                  0, Hkv, G * SS, v_sh, G * o_sh, 0, dtype, dtype, NKL_GEMM_BLOCKED, stream);
+    if (rc) return rc;
+  }
+  return NKL_OK;
+}
+
 extern "C" int nkl_attention_naive(const void* q, const void* k, const void* v, void* o, void* workspace,
                                    size_t workspace_bytes, int H, int S, int d, long q_sh, long q_ss, long k_sh,
                                    long k_ss, long v_sh, long v_ss, long o_sh, long o_ss, float scale, int dtype,
                                    void* stream) {
   const long strides[8] = {q_sh, q_ss, k_sh, k_ss, v_sh, v_ss, o_sh, o_ss};
-  int rc = check_attn("nkl_attention_naive", q, k, v, o, H, S, d, dtype, strides);
-  if (rc) return rc;
-  if (H == 0 || S == 0) return NKL_OK;
-  const size_t need = nkl_attention_naive_workspace_bytes(H, S, dtype);
-  if (!workspace || workspace_bytes < need)
-    return set_error(NKL_EWORKSPACE, "nkl_attention_naive: workspace of %zu bytes needed, %zu given", need,
-                     workspace_bytes);
-  const size_t n = (size_t)H * S * S;
-  float* sc = static_cast<float*>(workspace);
-  void* pr = static_cast<char*>(workspace) + (n * 4 + 255) / 256 * 256;
-  hipStream_t st = (hipStream_t)stream;
-  const long SS = (long)S * S;
-  // pass 1: scores[h] = Q[h] . K[h]^T (fp32)
-  rc = nkl_gemm(q, k, sc, nullptr, S, S, d, q_ss, k_ss, S, 0, 1, H, q_sh, k_sh, SS, 0, dtype, NKL_F32,
-                NKL_GEMM_BLOCKED, stream);
-  if (rc) return rc;
-  // pass 2: scale, mask, row softmax -> P
-  const dim3 grid((unsigned)(((long)H * S + 3) / 4)), block(256);
-  if (dtype == NKL_BF16)
-    masked_softmax_kernel<bf16><<<grid, block, 0, st>>>(sc, static_cast<bf16*>(pr), H, S, scale);
-  else
-    masked_softmax_kernel<float><<<grid, block, 0, st>>>(sc, static_cast<float*>(pr), H, S, scale);
-  rc = check_launch("nkl_attention_naive(softmax)");
-  if (rc) return rc;
-  // pass 3: O[h] = P[h] . V[h]
-  return nkl_gemm(pr, v, o, nullptr, S, d, S, S, v_ss, o_ss, 0, 0, H, SS, v_sh, o_sh, 0, dtype, dtype,
-                  NKL_GEMM_BLOCKED, stream);
+  return naive_entry("nkl_attention_naive", q, k, v, o, workspace, workspace_bytes, H, H > 0 ? H : 1, S, d, strides,
+                     scale, dtype, stream);
+}
+
+extern "C" int nkl_attention_naive_gqa(const void* q, const void* k, const void* v, void* o, void* workspace,
+                                       size_t workspace_bytes, int H, int Hkv, int S, int d, long q_sh, long q_ss,
+                                       long k_sh, long k_ss, long v_sh, long v_ss, long o_sh, long o_ss, float scale,
+                                       int dtype, void* stream) {
+  const long strides[8] = {q_sh, q_ss, k_sh, k_ss, v_sh, v_ss, o_sh, o_ss};
+  return naive_entry("nkl_attention_naive_gqa", q, k, v, o, workspace, workspace_bytes, H, Hkv, S, d, strides, scale,
+                     dtype, stream);
 }

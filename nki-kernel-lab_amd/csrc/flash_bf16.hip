@@ -241,7 +241,8 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
       q[f] = __builtin_bit_cast(bf16x8, ld16_or_zero(Q, (long)qrow * p.q_ss + dd, qrow < S && dd < dlim));
     }
   };
-  // Loads of one tensor (K or V) for step `it` of this team within segment sg.
+  // Loads of one tensor (K or V) for step `it` of this team within segment sg
+  // (K/V head hh / group: grouped-query attention shares a K/V head).
   auto gload = [&](const Seg& sg, int it, const void* base, long sh, long ss, const int (&goff)[CH],
                    uint4 (&rr)[CH]) __attribute__((always_inline)) {
     const int tj = sg.t0 + team + NT * it;
@@ -249,7 +250,8 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
     const int nkeys = tj < sg.t1 ? min(BN, S - k0) : 0;
     const int bytes = nkeys > 0 ? 2 * ((nkeys - 1) * (int)ss + dlim) : 0;
     const __amdgpu_buffer_rsrc_t src = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(static_cast<const bf16*>(base) + (long)sg.hh * sh + (long)k0 * ss), (short)0, bytes, kBufferFlags);
+        (void*)(static_cast<const bf16*>(base) + (long)(sg.hh / p.group) * sh + (long)k0 * ss), (short)0, bytes,
+        kBufferFlags);
 #pragma unroll
     for (int i = 0; i < CH; ++i)
       rr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(src, goff[i], 0, 0));
@@ -751,10 +753,10 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
     const int kbytes = nkeys > 0 ? 2 * ((nkeys - 1) * (int)p.k_ss + dlim) : 0;
     const int vbytes = nkeys > 0 ? 2 * ((nkeys - 1) * (int)p.v_ss + dlim) : 0;
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(static_cast<const bf16*>(p.k) + (long)sg.hh * p.k_sh + (long)k0 * p.k_ss), (short)0, kbytes,
+        (void*)(static_cast<const bf16*>(p.k) + (long)(sg.hh / p.group) * p.k_sh + (long)k0 * p.k_ss), (short)0, kbytes,
         kBufferFlags);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(static_cast<const bf16*>(p.v) + (long)sg.hh * p.v_sh + (long)k0 * p.v_ss), (short)0, vbytes,
+        (void*)(static_cast<const bf16*>(p.v) + (long)(sg.hh / p.group) * p.v_sh + (long)k0 * p.v_ss), (short)0, vbytes,
         kBufferFlags);
     unsigned char* sb = lds + st * W1_STAGEB;
 #pragma unroll

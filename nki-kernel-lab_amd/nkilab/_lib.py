@@ -38,6 +38,14 @@ SIGNATURES = {
     "nkl_flash_attn_causal_ws": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_size, _vp, _c_size, _c_int, _c_int, _c_int,
                                           _c_long, _c_long, _c_long, _c_long, _c_long, _c_long, _c_long, _c_long,
                                           _c_float, _c_int, _vp]),
+    "nkl_flash_attn_causal_gqa": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_size, _vp, _c_size, _c_int, _c_int, _c_int,
+                                           _c_int, _c_long, _c_long, _c_long, _c_long, _c_long, _c_long, _c_long,
+                                           _c_long, _c_float, _c_int, _vp]),
+    "nkl_attention_naive_gqa": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_size, _c_int, _c_int, _c_int, _c_int, _c_long,
+                                         _c_long, _c_long, _c_long, _c_long, _c_long, _c_long, _c_long, _c_float,
+                                         _c_int, _vp]),
+    "nkl_rope": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _c_long, _c_long, _c_long, _c_long, _c_int, _c_float,
+                          _c_int, _vp]),
     "nkl_attention_naive_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int]),
     "nkl_attention_naive": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_size, _c_int, _c_int, _c_int, _c_long, _c_long,
                                      _c_long, _c_long, _c_long, _c_long, _c_long, _c_long, _c_float, _c_int, _vp]),

@@ -21,6 +21,9 @@ Differences from the reference's host glue, none of which changes the math:
   * in bf16 the gate and up projections and the SwiGLU between them
     (model.py:88) are one GEMM over the two weights interleaved in groups of
     32 rows, with SwiGLU in its epilogue (the same values as the three calls);
+  * ``BlockConfig(n_kv_heads=..., rope_base=...)`` adds grouped-query
+    attention and rotary embeddings, which the reference lacks (README.md:89);
+    both default off, giving the reference's block;
   * ``compute_dtype="bfloat16"`` runs the block in bf16 with an fp32 residual
     stream (the GEMMs that feed the residual emit fp32).  The default keeps
     the reference's behaviour: everything in x's dtype.
@@ -43,10 +46,29 @@ class BlockConfig:
     n_heads: int = 4
     d_ff: int = 1024
     eps: float = 1e-6
+    # Options the reference lacks (README.md:89); the defaults keep its block.
+    n_kv_heads: int | None = None   # grouped-query attention: K/V heads (dividing n_heads)
+    rope_base: float | None = None  # rotary embedding of q and k (rotate-half layout)
 
     @property
     def head_dim(self) -> int:
         return self.d_model // self.n_heads
+
+    @property
+    def kv_heads(self) -> int:
+        return self.n_kv_heads or self.n_heads
+
+
+def rope_reference(x: torch.Tensor, base: float, pos0: int = 0) -> torch.Tensor:
+    """RoPE of x [..., S, d] in PyTorch (rotate-half layout, fp32 angles): the
+    eager block's rotary embedding."""
+    S, d = x.shape[-2], x.shape[-1]
+    half = d // 2
+    inv = base ** (-2.0 * torch.arange(half, dtype=torch.float64, device=x.device) / d)
+    a = ((pos0 + torch.arange(S, dtype=torch.float64, device=x.device))[:, None] * inv[None, :]).float()
+    c, s = torch.cos(a), torch.sin(a)
+    x1, x2 = x[..., :half].float(), x[..., half:].float()
+    return torch.cat((x1 * c - x2 * s, x2 * c + x1 * s), dim=-1).to(x.dtype)
 
 
 class RMSNorm(nn.Module):
@@ -71,7 +93,9 @@ class DecoderBlock(nn.Module):
         d, f = cfg.d_model, cfg.d_ff
         self.norm1 = RMSNorm(d, cfg.eps)
         self.norm2 = RMSNorm(d, cfg.eps)
-        self.wqkv = nn.Linear(d, 3 * d, bias=False)
+        if cfg.n_heads % cfg.kv_heads:
+            raise ValueError(f"BlockConfig: n_kv_heads={cfg.n_kv_heads} must divide n_heads={cfg.n_heads}")
+        self.wqkv = nn.Linear(d, d + 2 * cfg.kv_heads * cfg.head_dim, bias=False)
         self.wo = nn.Linear(d, d, bias=False)
         self.wg = nn.Linear(d, f, bias=False)
         self.wu = nn.Linear(d, f, bias=False)
@@ -83,9 +107,14 @@ class DecoderBlock(nn.Module):
 
     def forward(self, x):  # x: [S, d_model]
         S, d = x.shape
-        H, hd = self.cfg.n_heads, self.cfg.head_dim
-        heads = lambda t: t.reshape(S, H, hd).transpose(0, 1)  # noqa: E731  [H, S, hd]
-        q, k, v = (heads(t) for t in self.wqkv(self.norm1(x)).chunk(3, dim=-1))
+        H, hd, Hkv = self.cfg.n_heads, self.cfg.head_dim, self.cfg.kv_heads
+        qkv = self.wqkv(self.norm1(x))
+        q = qkv[:, :d].reshape(S, H, hd).transpose(0, 1)  # [H, S, hd]
+        k, v = (t.reshape(S, Hkv, hd).transpose(0, 1) for t in qkv[:, d:].chunk(2, dim=-1))
+        if self.cfg.rope_base is not None:
+            q, k = rope_reference(q, self.cfg.rope_base), rope_reference(k, self.cfg.rope_base)
+        if Hkv != H:
+            k, v = (t.repeat_interleave(H // Hkv, dim=0) for t in (k, v))
         attn = F.scaled_dot_product_attention(q, k, v, is_causal=True)
         x = x + self.wo(attn.transpose(0, 1).reshape(S, d))
         h = self.norm2(x)
@@ -147,9 +176,16 @@ def nki_forward(block: DecoderBlock, x, attention_variant: str = "flash_pipeline
 
     h = torch.empty((S, d), dtype=cdt, device=dev)
     ops.rmsnorm_into(xt, g1, h, cfg.eps)
-    qkv = torch.empty((S, 3 * d), dtype=cdt, device=dev)
+    Hkv = cfg.kv_heads
+    kvd = Hkv * hd
+    qkv = torch.empty((S, d + 2 * kvd), dtype=cdt, device=dev)
     ops.linear_into(h, W["wqkv"], qkv)
-    q, k, v = (qkv[:, i * d:(i + 1) * d].view(S, H, hd).transpose(0, 1) for i in range(3))
+    q = qkv[:, :d].view(S, H, hd).transpose(0, 1)
+    k = qkv[:, d:d + kvd].view(S, Hkv, hd).transpose(0, 1)
+    v = qkv[:, d + kvd:].view(S, Hkv, hd).transpose(0, 1)
+    if cfg.rope_base is not None:  # in place on the q and k columns of qkv
+        ops.rope_into(q, q, cfg.rope_base)
+        ops.rope_into(k, k, cfg.rope_base)
     a = torch.empty((S, d), dtype=cdt, device=dev)
     ops.attention_into(q, k, v, a.view(S, H, hd).transpose(0, 1), variant=attention_variant)
     x1 = torch.empty((S, d), dtype=rdt, device=dev)

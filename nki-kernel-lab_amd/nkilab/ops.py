@@ -157,6 +157,30 @@ def matmul(a, b, variant: str = "blocked"):
     return from_device(c, kind)
 
 
+# ---------------------------------------------------------------- RoPE --
+
+def rope_into(x: torch.Tensor, y: torch.Tensor, base: float = 10000.0, pos0: int = 0) -> torch.Tensor:
+    """Rotary position embedding (rotate-half layout) of x [H, S, d] into y
+    (which may be x): elements i and i + d/2 of row s rotate by
+    (pos0 + s) * base^(-2 i / d).  Any strides along H and S; d contiguous."""
+    if x.dim() != 3 or y.shape != x.shape or x.dtype != y.dtype:
+        raise ValueError(f"rope_into: x {tuple(x.shape)} and y {tuple(y.shape)} must be equal [H, S, d] tensors")
+    H, S, d = x.shape
+    for t in (x, y):
+        if t.stride(2) != 1 and d > 1:
+            raise ValueError("rope_into: the head dim must be contiguous")
+    _lib.call("nkl_rope", ptr(x), ptr(y), H, S, d, x.stride(0), x.stride(1), y.stride(0), y.stride(1), int(pos0),
+              float(base), dtype_code(x.dtype), stream_handle())
+    return y
+
+
+def rope(x, base: float = 10000.0, pos0: int = 0):
+    """RoPE of x [H, S, d] (NumPy or torch); returns a new array of x's kind."""
+    tx, kind = to_device(x)
+    y = torch.empty_like(tx)
+    return from_device(rope_into(tx, y, base, pos0), kind)
+
+
 # ------------------------------------------------------------- row ops --
 
 def _as_rows(t: torch.Tensor) -> tuple[torch.Tensor, int, int, int]:
@@ -283,10 +307,16 @@ def _attn_operand(t: torch.Tensor, E: int) -> torch.Tensor:
 
 def attention_into(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
                    variant: str = "flash_pipelined", scale: float | None = None) -> torch.Tensor:
-    """Causal attention into o; q, k, v, o: [H, S, d] GPU tensors, any strides along
-    H and S (d contiguous).  d must be a multiple of 8 (bf16) / 4 (fp32)."""
+    """Causal attention into o; q, o: [H, S, d] and k, v: [Hkv, S, d] GPU tensors
+    (Hkv = H, or a divisor of H for grouped-query attention: query head h reads
+    K/V head h // (H / Hkv)), any strides along heads and S (d contiguous).
+    d must be a multiple of 8 (bf16) / 4 (fp32)."""
     spec = ATTENTION_VARIANTS[variant]
     H, S, d = q.shape
+    Hkv = k.shape[0]
+    if k.shape != v.shape or k.shape[1:] != q.shape[1:] or Hkv < 1 or H % Hkv:
+        raise ValueError(f"attention_into: k, v {tuple(k.shape)}, {tuple(v.shape)} must be [Hkv, S, d] with Hkv "
+                         f"dividing the {H} query heads of q {tuple(q.shape)}")
     if scale is None:
         scale = 1.0 / math.sqrt(d)
     E = 8 if q.dtype == torch.bfloat16 else 4
@@ -296,9 +326,17 @@ def attention_into(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.T
     strides = (q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
                out.stride(0), out.stride(1))
     dt = dtype_code(q.dtype)
+    gqa = Hkv != H
     if spec.path == "flash":
         nbytes = _lib.lib().nkl_flash_attn_causal_workspace_bytes(H, S, d, dt)
-        if nbytes:
+        if gqa:
+            ws = cnt = None
+            if nbytes:
+                ws, cnt = _flash_scratch(nbytes, _lib.lib().nkl_flash_attn_causal_counter_bytes(H, S, dt), q.device)
+            _lib.call("nkl_flash_attn_causal_gqa", ptr(q), ptr(k), ptr(v), ptr(out), ptr(ws),
+                      ws.numel() if ws is not None else 0, ptr(cnt), cnt.numel() * 4 if cnt is not None else 0,
+                      H, Hkv, S, d, *strides, float(scale), dt, stream_handle())
+        elif nbytes:
             ws, cnt = _flash_scratch(nbytes, _lib.lib().nkl_flash_attn_causal_counter_bytes(H, S, dt), q.device)
             _lib.call("nkl_flash_attn_causal_ws", ptr(q), ptr(k), ptr(v), ptr(out), ptr(ws), ws.numel(), ptr(cnt),
                       cnt.numel() * 4, H, S, d, *strides, float(scale), dt, stream_handle())
@@ -308,8 +346,12 @@ def attention_into(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.T
     else:
         nbytes = _lib.lib().nkl_attention_naive_workspace_bytes(H, S, dt)
         ws = workspace(nbytes, q.device)
-        _lib.call("nkl_attention_naive", ptr(q), ptr(k), ptr(v), ptr(out), ptr(ws), nbytes, H, S, d, *strides,
-                  float(scale), dt, stream_handle())
+        if gqa:
+            _lib.call("nkl_attention_naive_gqa", ptr(q), ptr(k), ptr(v), ptr(out), ptr(ws), nbytes, H, Hkv, S, d,
+                      *strides, float(scale), dt, stream_handle())
+        else:
+            _lib.call("nkl_attention_naive", ptr(q), ptr(k), ptr(v), ptr(out), ptr(ws), nbytes, H, S, d, *strides,
+                      float(scale), dt, stream_handle())
     if out is not o:
         o.copy_(out)
     return o
@@ -317,6 +359,8 @@ def attention_into(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.T
 
 def attention(q, k, v, variant: str = "flash_pipelined"):
     """Causal attention. q, k, v: [H, S, d] (ops.py:77-91); scale 1/sqrt(d).
+    k and v may also have fewer heads Hkv dividing H (grouped-query attention:
+    query head h uses K/V head h // (H / Hkv)), which the reference lacks.
 
     The reference pads S to a multiple of 128 and transposes q and k on the
     host; the HIP kernels take [H, S, d] as is and bound-check ragged S, so
@@ -329,9 +373,10 @@ def attention(q, k, v, variant: str = "flash_pipelined"):
     tv, _ = to_device(v)
     if not (tq.dtype == tk.dtype == tv.dtype):
         raise TypeError("attention: q, k and v must share a dtype")
-    if tq.dim() != 3 or tk.shape != tq.shape or tv.shape != tq.shape:
-        raise ValueError(f"attention: q, k, v must all be [H, S, d], got {tuple(tq.shape)}, {tuple(tk.shape)}, "
-                         f"{tuple(tv.shape)}")
+    if (tq.dim() != 3 or tk.shape != tv.shape or tk.dim() != 3 or tk.shape[1:] != tq.shape[1:]
+            or tk.shape[0] < 1 or tq.shape[0] % tk.shape[0]):
+        raise ValueError(f"attention: q must be [H, S, d] and k, v [Hkv, S, d] with Hkv dividing H, got "
+                         f"{tuple(tq.shape)}, {tuple(tk.shape)}, {tuple(tv.shape)}")
     H, S, d = tq.shape
     assert d <= 128, "head dim must be <= 128"
     E = 8 if tq.dtype == torch.bfloat16 else 4

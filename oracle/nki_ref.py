@@ -25,6 +25,10 @@ How each function is pinned (tests/test_oracle.py):
                        QK^T tile count n(n+1)/2 vs n^2 (tests/test_attention.py,
                        tests/test_profiler.py:51-61)
   nki_forward_ref      torch DecoderBlock, atol 1e-5 fp32 (tests/test_model.py:8-17)
+  rope                 (not in the reference) identity at position 0; each (i, i + d/2)
+                       pair keeps its norm; <rope(q, m), rope(k, n)> depends on m - n
+                       only; equals an independent torch float64 rotate-half formula
+  GQA in ops_attention (not in the reference) SDPA on K/V heads repeated H / Hkv times
 
 Parity unpinned at the bit level (no reference test or fixture fixes them, and
 the NKI simulator is not installable here): the simulator's exp / rsqrt /
@@ -51,7 +55,7 @@ __all__ = [
     "matmul_naive", "matmul_blocked", "ops_matmul", "softmax_fused", "softmax_unfused",
     "rmsnorm_fused", "swiglu_fused", "attention_naive", "flash_attention",
     "flash_attention_kv_resident", "flash_attention_balanced", "flash_attention_pipelined",
-    "ATTENTION_VARIANTS", "ops_attention", "nki_forward_ref", "rel_err", "causal_flops",
+    "ATTENTION_VARIANTS", "ops_attention", "nki_forward_ref", "rel_err", "causal_flops", "rope",
 ]
 
 
@@ -357,10 +361,14 @@ ATTENTION_VARIANTS = {
 def ops_attention(q, k, v, variant: str = "flash_pipelined", dtype: str = F32,
                   stats: dict | None = None) -> np.ndarray:
     """ops.py:77-91: pad S to a multiple of 128 at the end, qT/kT = [H, d, S],
-    scale = 1/sqrt(d), run, crop."""
+    scale = 1/sqrt(d), run, crop.  k and v with Hkv < H heads (grouped-query
+    attention, which the reference lacks) serve query heads h with K/V head
+    h // (H / Hkv): they are repeated to H heads first."""
     fn = ATTENTION_VARIANTS[variant]
     q, k, v = (np.asarray(t, np.float32) for t in (q, k, v))
     H, S, d = q.shape
+    if k.shape[0] != H:
+        k, v = (np.repeat(t, H // t.shape[0], axis=0) for t in (k, v))
     Sp = math.ceil(S / T) * T
     if Sp != S:
         pad = ((0, 0), (0, Sp - S), (0, 0))
@@ -371,20 +379,46 @@ def ops_attention(q, k, v, variant: str = "flash_pipelined", dtype: str = F32,
     return o[:, :S, :]
 
 
+# ------------------------------------------------------------------ RoPE --
+
+def rope(x, pos0: int = 0, base: float = 10000.0, dtype: str = F32) -> np.ndarray:
+    """Rotary position embedding, rotate-half layout: RoFormer (Su et al., 2021)
+    as GPT-NeoX and Llama apply it.  Not in the reference (README.md:89 lists it
+    as not done).  x [H, S, d], d even: elements i < d/2 and i + d/2 of row s
+    rotate by (pos0 + s) * base^(-2 i / d), computed in float64; one rounding."""
+    x = np.asarray(x, np.float32)
+    H, S, d = x.shape
+    half = d // 2
+    inv = base ** (-2.0 * np.arange(half, dtype=np.float64) / d)
+    a = (pos0 + np.arange(S, dtype=np.float64))[:, None] * inv[None, :]
+    c, s = np.cos(a), np.sin(a)
+    x1, x2 = x[..., :half].astype(np.float64), x[..., half:].astype(np.float64)
+    y = np.concatenate([x1 * c - x2 * s, x2 * c + x1 * s], axis=-1)
+    return cast(y.astype(np.float32), dtype)
+
+
 # -------------------------------------------------------------- decoder --
 
 def nki_forward_ref(params: dict, x, n_heads: int, eps: float = 1e-6, attention_variant: str = "flash_pipelined",
-                    dtype: str = F32) -> np.ndarray:
+                    dtype: str = F32, n_kv_heads: int | None = None, rope_base: float | None = None) -> np.ndarray:
     """model.py:70-89 on the oracle kernels.  params: numpy arrays 'wqkv', 'wo', 'wg',
-    'wu', 'wd' in nn.Linear layout [out, in], and 'norm1', 'norm2' [d]."""
+    'wu', 'wd' in nn.Linear layout [out, in], and 'norm1', 'norm2' [d].  Options the
+    reference lacks: n_kv_heads < n_heads (grouped-query attention; wqkv then
+    projects to d + 2 n_kv_heads head_dim) and rope_base (RoPE on q and k)."""
     x = np.asarray(x, np.float32)
     S, d = x.shape
     hd = d // n_heads
+    hkv = n_kv_heads or n_heads
+    kvd = hkv * hd
     w = lambda name: cast(np.asarray(params[name], np.float32).T.copy(), dtype)  # noqa: E731  [in, out]
     g = lambda name: cast(params[name], dtype)  # noqa: E731
     h = rmsnorm_fused(x, g("norm1"), eps, dtype)
     qkv = ops_matmul(h, w("wqkv"), dtype=dtype)
-    q, k, v = (qkv[:, i * d:(i + 1) * d].reshape(S, n_heads, hd).transpose(1, 0, 2) for i in range(3))
+    q = qkv[:, :d].reshape(S, n_heads, hd).transpose(1, 0, 2)
+    k = qkv[:, d:d + kvd].reshape(S, hkv, hd).transpose(1, 0, 2)
+    v = qkv[:, d + kvd:d + 2 * kvd].reshape(S, hkv, hd).transpose(1, 0, 2)
+    if rope_base is not None:
+        q, k = rope(q, 0, rope_base, dtype), rope(k, 0, rope_base, dtype)
     a = ops_attention(q, k, v, attention_variant, dtype)
     x = cast(x + ops_matmul(a.transpose(1, 0, 2).reshape(S, d), w("wo"), dtype=dtype), dtype)
     h = rmsnorm_fused(x, g("norm2"), eps, dtype)

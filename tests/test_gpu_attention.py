@@ -241,3 +241,42 @@ def test_long_context_32x16384_bf16_sampled():
     for hi in range(3):
         ref = _rows_reference(qn, kn, vn, hi, rows, 1.0 / math.sqrt(d))
         assert rel_err(on[hi, rows], ref) <= 3e-3
+
+
+# ------------------------------------ grouped-query attention (not in the reference) --
+
+@pytest.mark.parametrize("variant", ["naive", "flash_pipelined"])
+@pytest.mark.parametrize("H,Hkv,S,d", [(8, 2, 300, 128), (4, 1, 129, 64), (6, 3, 77, 32), (16, 4, 1024, 128)])
+def test_gqa_attention_matches_sdpa_on_repeated_kv(rng, variant, H, Hkv, S, d):
+    """K/V with Hkv heads serve H query heads (head h uses K/V head h // (H / Hkv)),
+    fp32 and bf16, against SDPA on K/V repeated to H heads and against the oracle."""
+    from nkilab import ops
+
+    q = rng.standard_normal((H, S, d)).astype(np.float32)
+    k, v = (rng.standard_normal((Hkv, S, d)).astype(np.float32) for _ in range(2))
+    rep = lambda t: np.repeat(t, H // Hkv, axis=0)  # noqa: E731
+    ref = _sdpa_cpu(q, rep(k), rep(v))
+    out = ops.attention(q, k, v, variant=variant)
+    assert rel_err(out, ref) < 1e-5, ("fp32", variant)
+    qb, kb, vb = (_bf(t) for t in (q, k, v))
+    outb = _np(ops.attention(qb, kb, vb, variant=variant))
+    refb = _sdpa_cpu(_np(qb), rep(_np(kb)), rep(_np(vb)))
+    assert rel_err(outb, refb) < 1e-2, ("bf16", variant)
+    assert rel_err(outb, O.ops_attention(_np(qb), _np(kb), _np(vb), variant, O.BF16)) < 1e-2
+
+
+@pytest.mark.parametrize("kernel,qb,schedule", [("teams", "128", "balanced"), ("teams", "64", "balanced"),
+                                                ("teams", "128", "pairs"), ("teams", "128", "block"),
+                                                ("w64", "128", "balanced"), ("teams4", "64", "balanced")])
+def test_gqa_bf16_every_kernel_and_schedule(rng, monkeypatch, kernel, qb, schedule):
+    from nkilab import ops
+
+    monkeypatch.setenv("NKL_FLASH_KERNEL", kernel)
+    monkeypatch.setenv("NKL_FLASH_SCHEDULE", schedule)
+    monkeypatch.setenv("NKL_FLASH_QB", qb)
+    H, Hkv, S, d = 8, 2, 1537, 128
+    q = _bf(rng.standard_normal((H, S, d)))
+    k, v = (_bf(rng.standard_normal((Hkv, S, d))) for _ in range(2))
+    out = _np(ops.attention(q, k, v))
+    ref = _sdpa_cpu(_np(q), *(np.repeat(_np(t), H // Hkv, axis=0) for t in (k, v)))
+    assert rel_err(out, ref) < 1e-2, (kernel, qb, schedule)

@@ -103,3 +103,20 @@ def test_decoder_bf16_matches_oracle_composition():
     params = {n: getattr(block, n).weight.detach().numpy() for n in ("wqkv", "wo", "wg", "wu", "wd", "norm1", "norm2")}
     ref = O.nki_forward_ref(params, x, cfg.n_heads, cfg.eps, "flash_pipelined", O.BF16)
     assert rel_err(out, ref) < 2e-2
+
+
+@pytest.mark.parametrize("n_kv_heads,rope_base", [(2, None), (None, 10000.0), (1, 500000.0)])
+def test_decoder_gqa_rope_matches_pytorch(n_kv_heads, rope_base):
+    """Grouped-query attention and rotary embeddings (not in the reference) end to
+    end: fp32 within 1e-3 of the eager block, bf16 within bf16 tolerance."""
+    from nkilab.model import BlockConfig, DecoderBlock, nki_forward
+
+    torch.manual_seed(0)
+    block = DecoderBlock(BlockConfig(n_kv_heads=n_kv_heads, rope_base=rope_base)).eval()
+    x = torch.randn(300, block.cfg.d_model)
+    with torch.no_grad():
+        ref = block(x).numpy()
+    out = nki_forward(block, x.numpy())
+    assert np.abs(out - ref).max() <= 1e-3 * np.abs(ref).max()
+    outb = nki_forward(block, x.cuda(), compute_dtype="bfloat16").float().cpu().numpy()
+    assert rel_err(outb, ref) < 2e-2

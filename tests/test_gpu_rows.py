@@ -164,3 +164,48 @@ def test_strided_rows_and_async_tensors(rng):
     out = ops.softmax(x)
     assert out.is_cuda
     np.testing.assert_allclose(_np(out), torch.softmax(x.cpu(), -1).numpy(), rtol=1e-5, atol=1e-6)
+
+
+# -------------------------------------------------- RoPE (not in the reference) --
+
+@pytest.mark.parametrize("dt", ["float32", "bfloat16"])
+@pytest.mark.parametrize("H,S,d,pos0,base", [(2, 300, 128, 0, 10000.0), (4, 65, 64, 1000, 500000.0),
+                                             (1, 7, 8, 5, 10000.0), (8, 2048, 128, 0, 10000.0)])
+def test_rope_matches_oracle(rng, dt, H, S, d, pos0, base):
+    """The RoPE kernel against the oracle (float64 angles).  fp32 outputs are
+    within the fp32 angle error (relative 2e-7 of the angle, times the pair's
+    norm); bf16 outputs within one bf16 step of the oracle's value plus that."""
+    import torch
+
+    import oracle as O
+    from nkilab import ops
+
+    x = rng.standard_normal((H, S, d)).astype(np.float32)
+    tdt = getattr(torch, dt)
+    xt = torch.from_numpy(x).to(tdt).cuda()
+    out = ops.rope_into(xt, torch.empty_like(xt), base, pos0).float().cpu().numpy()
+    ref = O.rope(xt.float().cpu().numpy(), pos0, base, O.F32)
+    # fp32 angles: relative error ~2e-7 of (pos0 + s) rad, times the pair's norm
+    angle_floor = 1e-5 + 4e-7 * (pos0 + S) * np.abs(x).max()
+    if dt == "float32":
+        assert np.abs(out - ref).max() <= angle_floor
+    else:
+        assert_within_bf16_ulps(out, ref, 1, floor=angle_floor)
+
+
+def test_rope_in_place_on_strided_views(rng):
+    """In place on the q columns of a packed [S, 3 d] qkv buffer (the decoder's
+    layout), leaving the other columns untouched."""
+    import torch
+
+    import oracle as O
+    from nkilab import ops
+
+    S, H, hd = 200, 4, 64
+    qkv = torch.from_numpy(rng.standard_normal((S, 3 * H * hd)).astype(np.float32)).cuda()
+    before = qkv.clone()
+    q = qkv[:, :H * hd].view(S, H, hd).transpose(0, 1)
+    ops.rope_into(q, q, 10000.0)
+    ref = O.rope(before[:, :H * hd].view(S, H, hd).transpose(0, 1).cpu().numpy(), 0, 10000.0)
+    assert np.abs(q.cpu().numpy() - ref).max() < 1e-4
+    assert torch.equal(qkv[:, H * hd:], before[:, H * hd:])

@@ -102,6 +102,32 @@ def test_gemm_swiglu_abi_checks():
     assert L.nkl_gemm_swiglu(None, None, None, 0, 64, 64, 64, 64, 64, 1, None) == 0   # empty
 
 
+def test_rope_and_gqa_abi_checks():
+    from nkilab import _lib
+
+    L = _lib.lib()
+    assert L.nkl_rope(None, None, 1, 4, 7, 7, 7, 7, 7, 0, ctypes.c_float(1e4), 0, None) == -1  # odd d
+    assert b"even" in L.nkl_last_error_string()
+    assert L.nkl_rope(None, None, 1, 4, 8, 8, 8, 8, 8, 0, ctypes.c_float(1.0), 0, None) == -1  # base
+    assert L.nkl_rope(None, None, 1, 4, 8, 8, 8, 8, 8, 0, ctypes.c_float(1e4), 9, None) == -2  # dtype
+    assert L.nkl_rope(None, None, 0, 4, 8, 8, 8, 8, 8, 0, ctypes.c_float(1e4), 0, None) == 0   # empty
+    assert L.nkl_flash_attn_causal_gqa(None, None, None, None, None, 0, None, 0, 4, 3, 16, 64, 0, 64, 0, 64, 0, 64,
+                                       0, 64, ctypes.c_float(0.1), 1, None) == -1
+    assert b"divide" in L.nkl_last_error_string()
+    assert L.nkl_attention_naive_gqa(None, None, None, None, None, 0, 4, 0, 16, 64, 0, 64, 0, 64, 0, 64, 0, 64,
+                                     ctypes.c_float(0.1), 1, None) == -1
+
+
+def test_block_config_options_default_to_the_reference_block():
+    from nkilab.model import BlockConfig, DecoderBlock
+
+    cfg = BlockConfig()
+    assert cfg.n_kv_heads is None and cfg.rope_base is None and cfg.kv_heads == cfg.n_heads
+    assert DecoderBlock(cfg).wqkv.weight.shape == (3 * 256, 256)
+    with pytest.raises(ValueError):
+        DecoderBlock(BlockConfig(n_kv_heads=3))
+
+
 def test_psum_block_check():
     from nkilab import _lib
 

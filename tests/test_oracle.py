@@ -243,3 +243,81 @@ def test_oracle_reproduces_committed_golden_vectors():
 
 def test_exact_scale_is_reciprocal_sqrt():
     assert math.isclose(1.0 / math.sqrt(128), 0.08838834764831845)
+
+
+# ------------------------------------------------- RoPE and GQA (not in the reference) --
+
+def _torch_rope_rotate_half(x, pos0, base):
+    """An independent float64 statement in the form Hugging Face's Llama uses:
+    emb = cat(freqs, freqs); x * cos(emb) + rotate_half(x) * sin(emb)."""
+    x = torch.from_numpy(np.asarray(x, np.float64))
+    S, d = x.shape[-2], x.shape[-1]
+    inv = 1.0 / (base ** (torch.arange(0, d, 2, dtype=torch.float64) / d))
+    freqs = torch.outer(torch.arange(pos0, pos0 + S, dtype=torch.float64), inv)
+    emb = torch.cat((freqs, freqs), dim=-1)
+    x1, x2 = x[..., :d // 2], x[..., d // 2:]
+    rot = torch.cat((-x2, x1), dim=-1)
+    return (x * emb.cos() + rot * emb.sin()).numpy()
+
+
+@pytest.mark.parametrize("H,S,d,pos0,base", [(2, 7, 8, 0, 10000.0), (1, 33, 128, 100, 10000.0),
+                                             (3, 5, 64, 4090, 500000.0)])
+def test_rope_matches_rotate_half_form(rng, H, S, d, pos0, base):
+    x = rng.standard_normal((H, S, d)).astype(np.float32)
+    np.testing.assert_allclose(O.rope(x, pos0, base), _torch_rope_rotate_half(x, pos0, base), rtol=1e-5, atol=1e-5)
+
+
+def test_rope_properties(rng):
+    """Identity at position 0; every (i, i + d/2) pair keeps its norm; the dot
+    product of a rotated query and key depends only on their distance; and a
+    planted sign mistake in the oracle's rotation is caught by the
+    rotate-half comparison."""
+    d = 64
+    x = rng.standard_normal((1, 1, d)).astype(np.float32)
+    np.testing.assert_array_equal(O.rope(x, 0), x)
+    x2 = rng.standard_normal((2, 50, d)).astype(np.float32)
+    r2 = O.rope(x2, 17)
+    n_in = x2[..., :d // 2].astype(np.float64) ** 2 + x2[..., d // 2:].astype(np.float64) ** 2
+    n_out = r2[..., :d // 2].astype(np.float64) ** 2 + r2[..., d // 2:].astype(np.float64) ** 2
+    np.testing.assert_allclose(n_out, n_in, rtol=1e-5)
+    q, k = (rng.standard_normal((1, 1, d)).astype(np.float32) for _ in range(2))
+    dots = [float(np.sum(O.rope(q, m).astype(np.float64) * O.rope(k, m - 5))) for m in (5, 40, 300)]
+    np.testing.assert_allclose(dots, dots[0], rtol=1e-5)
+    # the oracle's rotation with the sine's sign flipped (a plausible slip):
+    # still norm-preserving, but the rotate-half comparison rejects it
+    half = d // 2
+    a = (17 + np.arange(50, dtype=np.float64))[:, None] * 10000.0 ** (-2.0 * np.arange(half) / d)
+    c, sn = np.cos(a), np.sin(a)
+    lo, hi = x2[..., :half].astype(np.float64), x2[..., half:].astype(np.float64)
+    flipped = np.concatenate([lo * c + hi * sn, hi * c - lo * sn], axis=-1)
+    ref = _torch_rope_rotate_half(x2, 17, 10000.0)
+    assert not np.allclose(flipped, ref, atol=1e-3)
+    np.testing.assert_allclose(r2, ref, atol=1e-5)
+
+
+@pytest.mark.parametrize("H,Hkv", [(4, 2), (4, 1), (6, 3)])
+def test_gqa_attention_repeats_kv_heads(rng, H, Hkv):
+    S, d = 150, 32
+    q = rng.standard_normal((H, S, d)).astype(np.float32)
+    k, v = (rng.standard_normal((Hkv, S, d)).astype(np.float32) for _ in range(2))
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        torch.from_numpy(q), *(torch.from_numpy(t).repeat_interleave(H // Hkv, dim=0) for t in (k, v)),
+        is_causal=True).numpy()
+    for variant in ("naive", "flash_pipelined"):
+        np.testing.assert_allclose(O.ops_attention(q, k, v, variant), ref, atol=2e-5)
+
+
+@pytest.mark.parametrize("n_kv_heads,rope_base", [(2, None), (None, 10000.0), (1, 500000.0)])
+def test_decoder_oracle_gqa_rope_matches_pytorch_block(n_kv_heads, rope_base):
+    from nkilab.model import BlockConfig, DecoderBlock
+
+    torch.manual_seed(0)
+    block = DecoderBlock(BlockConfig(n_kv_heads=n_kv_heads, rope_base=rope_base)).eval()
+    assert block.wqkv.weight.shape[0] == 256 + 2 * (n_kv_heads or 4) * 64
+    x = torch.randn(130, 256)
+    with torch.no_grad():
+        ref = block(x).numpy()
+    params = {n: getattr(block, n).weight.detach().numpy() for n in ("wqkv", "wo", "wg", "wu", "wd", "norm1", "norm2")}
+    out = O.nki_forward_ref(params, x.numpy(), 4, 1e-6, "flash_pipelined", n_kv_heads=n_kv_heads,
+                            rope_base=rope_base)
+    np.testing.assert_allclose(out, ref, atol=1e-5)
