@@ -617,8 +617,8 @@ __device__ __forceinline__ void wait_vm() {
 
 }  // namespace
 
-template <int QH, int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
+template <int QH, int NW, int OCC = 1>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
 void flash_bf16_w1_kernel(AttnArgs p, Work w) {
   static_assert((QH == 1 || QH == 2) && (NW == 2 || NW == 4), "32 or 64 queries per wavefront, 2 or 4 wavefronts");
   constexpr int D = 128, NQF = D / 16, NDB = D / 32, QW = 32 * QH, QB = QW * NW;
@@ -630,9 +630,10 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
   using MF = Mfma32<bf16>;
   __shared__ __align__(16) unsigned char lds[W1_NS * W1_STAGEB];
   __shared__ int arrival;
-  // Declaring an AGPR use makes the compiler select the MFMA form whose
-  // accumulators live in AGPRs, which keeps O there for the whole loop.
-  asm volatile("" ::: "a255");
+  // Alone on its SIMD (OCC = 1), declaring an AGPR use makes the compiler
+  // select the MFMA form whose accumulators live in AGPRs, which keeps O there
+  // for the whole loop.  Two per SIMD (OCC = 2) share 256 registers.
+  if constexpr (OCC == 1) asm volatile("" ::: "a255");
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wq = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1133,9 +1134,11 @@ int cu_count() {
 }
 
 // Kernels: teams of wavefronts sharing SIMDs (8 wavefronts per workgroup, or
-// 4 with two workgroups per CU), or one wavefront per SIMD with 32 queries (4
-// per workgroup) or 64 queries (2 or 4 per workgroup).
-enum Kern { kTeams = 0, kW32x4 = 1, kW64x2 = 2, kW64x4 = 3, kTeams4 = 4 };
+// 4 with two workgroups per CU); the software-pipelined kernel with one
+// wavefront per SIMD and 32 queries (4 per workgroup) or 64 queries (2 or 4
+// per workgroup); or that kernel with 32 queries at two wavefronts per SIMD
+// (256 registers each, two independent workgroups per CU).
+enum Kern { kTeams = 0, kW32x4 = 1, kW64x2 = 2, kW64x4 = 3, kTeams4 = 4, kW32x4x2 = 5 };
 
 // A launch configuration: queries per block, a schedule and a kernel.  The
 // teams kernel takes 64-query blocks (2 wavefronts x 4 teams, or x 2 teams in
@@ -1149,7 +1152,7 @@ struct Config {
 };
 
 // Resident workgroups per CU: two for the two-wavefront kernel, else one.
-int wgs_per_cu(int kern) { return kern == kW64x2 || kern == kTeams4 ? 2 : 1; }
+int wgs_per_cu(int kern) { return kern == kW64x2 || kern == kTeams4 || kern == kW32x4x2 ? 2 : 1; }
 
 Work plan(int H, int S, Config cfg) {
   Work w{};
@@ -1175,21 +1178,25 @@ Work plan(int H, int S, Config cfg) {
   return w;
 }
 
-// Schedule choice, from measured launches on MI355X.  With fewer than ~12
-// units of 128-query blocks per CU, 64-query blocks halve the unit and keep
-// every CU busy; up to ~1000 units per CU the balanced schedule wins (whole
-// blocks leave CUs idle or unevenly loaded); beyond that one workgroup per
-// pair of blocks balances as well and needs no partial states.
+// Schedule and kernel choice, from measured launches on MI355X (units of
+// 128-query blocks per CU): below 18, 64-query blocks halve the unit and keep
+// every CU busy (8 x 2048: 17); up to 200 the 8-wavefront teams kernel over
+// balanced ranges (whole blocks leave CUs idle or unevenly loaded); from 200
+// the software-pipelined kernel at two wavefronts per SIMD (d > 64), whose
+// steady state is faster and whose longer segments amortise its start-up;
+// from 1024 one workgroup per pair of blocks, which balances as well and
+// needs no partial states.
 // NKL_FLASH_SCHEDULE=block|pairs|balanced, NKL_FLASH_QB=64|128 and
-// NKL_FLASH_KERNEL=teams|w1|w64|w64x4 override the choice (tests, tuning);
+// NKL_FLASH_KERNEL=teams|teams4|w1|w1o2|w64|w64x4 override the choice (tests, tuning);
 // the one-wavefront-per-SIMD kernels take 64 < d <= 128 and fix the block.
 Config choose(int H, int S, int d) {
   const long cus = cu_count();
   const long nqb = (S + 127) / 128;
   const long units128 = (long)H * (2 * (nqb - 1) * nqb + (S - 1) / BN + 1);
-  Config cfg = units128 < 12 * cus ? Config{64, kBalanced, kTeams}
-               : units128 < 1024 * cus ? Config{128, kBalanced, kTeams}
-                                       : Config{128, kPairs, kTeams};
+  Config cfg = units128 < 18 * cus     ? Config{64, kBalanced, kTeams}
+               : units128 < 200 * cus  ? Config{128, kBalanced, kTeams}
+               : units128 < 1024 * cus ? Config{128, kBalanced, kW32x4x2}
+                                       : Config{128, kPairs, kW32x4x2};
   if (const char* f = getenv("NKL_FLASH_SCHEDULE")) {
     if (!strcmp(f, "block")) cfg.sched = kBlock;
     if (!strcmp(f, "pairs")) cfg.sched = kPairs;
@@ -1203,11 +1210,12 @@ Config choose(int H, int S, int d) {
     if (!strcmp(f, "teams")) cfg.kern = kTeams;
     if (!strcmp(f, "teams4")) cfg.kern = kTeams4;
     if (!strcmp(f, "w1")) cfg.kern = kW32x4;
+    if (!strcmp(f, "w1o2")) cfg.kern = kW32x4x2;
     if (!strcmp(f, "w64")) cfg.kern = kW64x2;
     if (!strcmp(f, "w64x4")) cfg.kern = kW64x4;
   }
   if (d <= 64 && cfg.kern != kTeams4) cfg.kern = kTeams;
-  if (cfg.kern == kW32x4 || cfg.kern == kW64x2) cfg.qb = 128;
+  if (cfg.kern == kW32x4 || cfg.kern == kW64x2 || cfg.kern == kW32x4x2) cfg.qb = 128;
   if (cfg.kern == kW64x4) cfg.qb = 256;
   return cfg;
 }
@@ -1229,9 +1237,9 @@ void launch(const AttnArgs& a, const Work& w, hipStream_t st) {
   flash_bf16_kernel<D, WPT, NT><<<dim3((unsigned)w.grid), dim3(64 * WPT * NT), 0, st>>>(a, w);
 }
 
-template <int QH, int NW>
+template <int QH, int NW, int OCC = 1>
 void launch_w(const AttnArgs& a, const Work& w, hipStream_t st) {
-  flash_bf16_w1_kernel<QH, NW><<<dim3((unsigned)w.grid), dim3(64 * NW), 0, st>>>(a, w);
+  flash_bf16_w1_kernel<QH, NW, OCC><<<dim3((unsigned)w.grid), dim3(64 * NW), 0, st>>>(a, w);
 }
 
 template <int D>
@@ -1281,9 +1289,11 @@ int flash_bf16_launch(const AttnArgs& a, void* workspace, size_t workspace_bytes
     w.part_bytes = (int)need;
     w.count = counters;
   }
-  if (cfg.kern == kW32x4 || cfg.kern == kW64x2 || cfg.kern == kW64x4) {
+  if (cfg.kern == kW32x4 || cfg.kern == kW64x2 || cfg.kern == kW64x4 || cfg.kern == kW32x4x2) {
     if (cfg.kern == kW32x4)
       launch_w<1, 4>(a, w, st);
+    else if (cfg.kern == kW32x4x2)
+      launch_w<1, 4, 2>(a, w, st);
     else if (cfg.kern == kW64x2)
       launch_w<2, 2>(a, w, st);
     else

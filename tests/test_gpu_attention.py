@@ -138,7 +138,7 @@ def test_flash_bf16_schedules(rng, monkeypatch, kernel, qb, schedule, H, S, d):
     np.testing.assert_allclose(out[:, 0], _np(v)[:, 0], atol=1e-2)  # query 0 sees only key 0
 
 
-@pytest.mark.parametrize("kernel", ["w1", "w64", "w64x4"])
+@pytest.mark.parametrize("kernel", ["w1", "w1o2", "w64", "w64x4"])
 @pytest.mark.parametrize("schedule", ["balanced", "pairs", "block"])
 @pytest.mark.parametrize("H,S,d", [(1, 1, 128), (3, 77, 128), (1, 300, 128), (2, 1537, 128), (5, 640, 96),
                                    (1, 129, 128), (2, 4096, 128), (4, 257, 72)])
@@ -156,7 +156,7 @@ def test_flash_bf16_one_wave_per_simd_kernel(rng, monkeypatch, kernel, schedule,
     np.testing.assert_allclose(out[:, 0], _np(v)[:, 0], atol=1e-2)
 
 
-@pytest.mark.parametrize("kernel", ["w1", "w64", "w64x4", "teams4"])
+@pytest.mark.parametrize("kernel", ["w1", "w1o2", "w64", "w64x4", "teams4"])
 def test_flash_bf16_one_wave_per_simd_config(monkeypatch, kernel):
     """8 x 2048 x 128 through each one-wavefront-per-SIMD kernel (balanced):
     within 3e-3 of fp32 SDPA."""
