@@ -14,6 +14,8 @@
 // kernel's 16-byte loads cannot address): each wavefront computes one 32x32
 // tile of C reading its operands straight from global memory at every K step
 // -- no on-chip reuse, like the reference's matmul_naive.
+#include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 #include "common.h"
@@ -261,7 +263,14 @@ __global__ __launch_bounds__(256) void gemm_naive_kernel(GemmArgs p) {
 // row r sits at chunk c ^ g_swz(r).  The swizzle keeps the 16-row b128
 // fragment reads (A, B^T) and the 4-row transposed b64 reads (B as [K, N],
 // read with ds_read_b64_tr_b16) free of bank conflicts.  One barrier per
-// K-step; 2x2 wavefronts of 32x32x16 MFMA tiles.
+// K-step; WGM x WGN wavefronts of 32x32x16 MFMA tiles.
+//
+// 2 x 2 wavefronts (256 threads, one per SIMD) for tiles up to 128 x 128;
+// 2 x 4 (512 threads, two per SIMD) for 256-row tiles.  A 128 x 128 tile
+// stages 32 KB per K-step for 2 MFLOP, ~64 B/clk per CU at the MFMA rate --
+// all an L2 channel set delivers; a 256 x 256 tile stages half that per flop.
+// With two 64 KB stages the next K-step's copies have one K-step (32 MFMAs
+// per wavefront, two wavefronts per SIMD) to land.
 
 namespace {
 
@@ -277,26 +286,31 @@ __device__ __forceinline__ void g_wait_vm() {
   __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+__device__ __forceinline__ void g_wait_lgkm0() { __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4)); }
+
 constexpr unsigned kOOB = 0x80000000u;  // a buffer offset past every range: the lane reads zeros
 
 }  // namespace
 
-template <typename TO, int BM, int BN, bool BT, int NS>
-__global__ __launch_bounds__(256) void gemm_dma_kernel(GemmArgs p) {
+template <typename TO, int BM, int BN, bool BT, int NS, int WGM = 2, int WGN = 2>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_dma_kernel(GemmArgs p) {
   using MF = Mfma32<bf16>;
+  constexpr int NW = WGM * WGN;
   constexpr int A_BYTES = BM * 128;
   constexpr int B_BYTES = BN * 128;  // BN rows of 128 B (B^T) or BN / 64 sub-tiles of 64 x 128 B
   constexpr int STAGE = A_BYTES + B_BYTES;
-  constexpr int A_PW = A_BYTES / 1024 / 4, B_PW = B_BYTES / 1024 / 4;  // DMA instructions per wavefront
+  constexpr int A_PW = A_BYTES / 1024 / NW, B_PW = B_BYTES / 1024 / NW;  // DMA instructions per wavefront
   constexpr int LPT = A_PW + B_PW;
-  constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
-  static_assert(A_PW >= 1 && B_PW >= 1, "tile too small");
+  constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
+  static_assert(A_PW >= 1 && B_PW >= 1 && A_PW * NW * 1024 == A_BYTES && B_PW * NW * 1024 == B_BYTES,
+                "tile too small");
+  static_assert(TM >= 1 && TN >= 1 && TM * 32 * WGM == BM && TN * 32 * WGN == BN, "wavefront tiles");
   static_assert((NS - 2) * LPT < 64, "vmcnt range");
   __shared__ __align__(16) unsigned char lds[NS * STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wid >> 1, wn = wid & 1;
+  const int wm = wid / WGN, wn = wid % WGN;
   const int tiles_m = (p.M + BM - 1) / BM, tiles_n = (p.N + BN - 1) / BN;
   int tm, tn;
   tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
@@ -379,29 +393,27 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(GemmArgs p) {
 
   // ---- fragment offsets within a stage (K-step sub-step ks = 0..3)
   const int lr = lane & 31, lg = lane >> 5;
-  int afo[TM][4], bfo[TN][4][2];
+  // The swizzle depends on row bits 1..3 only, so the 32-row tiles of a
+  // wavefront sit 4096 bytes apart: one offset per sub-step, plus 4096 i.
+  int afo[4], bto[4], bfo[TN][4][2];
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) afo[i][ks] = g_pos(wm * WM + i * 32 + lr, 2 * ks + lg);
-  {
+  for (int ks = 0; ks < 4; ++ks) {
+    afo[ks] = g_pos(wm * WM + lr, 2 * ks + lg);
+    bto[ks] = A_BYTES + g_pos(wn * WN + lr, 2 * ks + lg);
+  }
+  if constexpr (!BT) {
     const int i16 = lane & 15, g2 = (lane >> 4) & 1;
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        if constexpr (BT) {
-          bfo[j][ks][0] = A_BYTES + g_pos(wn * WN + j * 32 + lr, 2 * ks + lg);
-          bfo[j][ks][1] = 0;
-        } else {
-          // lane i of a 16-lane group reads row k (4 per read) at columns n .. n + 3
-          const int n = wn * WN + j * 32 + 16 * g2 + 4 * (i16 & 3);
-          const int sub = n / 64, nc = n % 64;
+        // lane i of a 16-lane group reads row k (4 per read) at columns n .. n + 3
+        const int n = wn * WN + j * 32 + 16 * g2 + 4 * (i16 & 3);
+        const int sub = n / 64, nc = n % 64;
 #pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const int krow = 16 * ks + 8 * lg + 4 * h + (i16 >> 2);
-            bfo[j][ks][h] = A_BYTES + sub * 8192 + g_pos(krow, nc / 8) + (nc % 8) * 2;
-          }
+        for (int h = 0; h < 2; ++h) {
+          const int krow = 16 * ks + 8 * lg + 4 * h + (i16 >> 2);
+          bfo[j][ks][h] = A_BYTES + sub * 8192 + g_pos(krow, nc / 8) + (nc % 8) * 2;
         }
       }
   }
@@ -414,105 +426,146 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(GemmArgs p) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
+  // Fragments of sub-step ks (16 K) of the stage at sb.
+  auto frags = [&](const unsigned char* sb, int ks, bf16x8 (&af)[TM], bf16x8 (&bfr)[TN])
+                   __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const bf16x8*>(sb + afo[ks] + 4096 * i);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      if constexpr (BT) {
+        bfr[j] = *reinterpret_cast<const bf16x8*>(sb + bto[ks] + 4096 * j);
+      } else {
+        typedef short shortx4 __attribute__((ext_vector_type(4)));
+        typedef __attribute__((address_space(3))) shortx4 lds_s4;
+        const shortx4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(sb + bfo[j][ks][0]));
+        const shortx4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(sb + bfo[j][ks][1]));
+        bfr[j] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+    }
+  };
+  auto mmas = [&](const bf16x8 (&af)[TM], const bf16x8 (&bfr)[TN]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = MF::mma(af[i], bfr[j], acc[i][j]);
+  };
+  // Every wavefront's copies of a stage have landed once each waited for its
+  // own (vmcnt) and all passed the barrier.  A bare s_barrier, not
+  // __syncthreads(): the latter's fence makes the compiler wait for every
+  // outstanding copy (vmcnt(0)), which would leave one stage in flight
+  // instead of NS - 1.  The signal fences keep the compiler from moving LDS
+  // accesses across the barrier; they emit no instruction.
+  auto barrier = [&]() __attribute__((always_inline)) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  };
+
+  // Software pipeline: the fragments of sub-step ks + 1 are read while the
+  // MFMAs of sub-step ks run; the stage hand-over (wait, barrier, next copy)
+  // sits between the reads and the MFMAs of the last sub-step, so the barrier
+  // wait overlaps MFMAs already issued.
   const int nk = (K + G_BK - 1) / G_BK;
 #pragma unroll
-  for (int s = 0; s < NS - 1; ++s) dma(s, s);
+  for (int s = 0; s < NS; ++s) dma(s, s);
+  g_wait_vm<(NS - 1) * LPT>();  // K-step 0 has landed
+  barrier();
+  bf16x8 fa[2][TM], fb[2][TN];
+  frags(lds, 0, fa[0], fb[0]);
 #pragma unroll 1
   for (int s = 0; s < nk; ++s) {
-    g_wait_vm<(NS - 2) * LPT>();  // K-step s has landed
-    __syncthreads();              // ... for every wavefront; all are done with K-step s-1
-    dma(s + NS - 1, (s + NS - 1) % NS);
     const unsigned char* sb = lds + (s % NS) * STAGE;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      bf16x8 af[TM], bfr[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const bf16x8*>(sb + afo[i][ks]);
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        if constexpr (BT) {
-          bfr[j] = *reinterpret_cast<const bf16x8*>(sb + bfo[j][ks][0]);
-        } else {
-          typedef short shortx4 __attribute__((ext_vector_type(4)));
-          typedef __attribute__((address_space(3))) shortx4 lds_s4;
-          const shortx4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(sb + bfo[j][ks][0]));
-          const shortx4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(sb + bfo[j][ks][1]));
-          bfr[j] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7));
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = MF::mma(af[i], bfr[j], acc[i][j]);
+    for (int ks = 0; ks < 3; ++ks) {
+      frags(sb, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of the MFMAs
+      mmas(fa[ks & 1], fb[ks & 1]);
+      __builtin_amdgcn_sched_barrier(0);
     }
+    g_wait_vm<(NS - 2) * LPT>();  // K-step s+1 has landed
+    g_wait_lgkm0();               // this wavefront's reads of K-step s are done
+    barrier();                    // ... for every wavefront
+    dma(s + NS, s % NS);          // into K-step s's stage
+    frags(lds + ((s + 1) % NS) * STAGE, 0, fa[0], fb[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    mmas(fa[1], fb[1]);
+    __builtin_amdgcn_sched_barrier(0);
   }
   __builtin_amdgcn_s_waitcnt(0);  // the copies of K-steps past K have landed
 
   // Epilogue: accumulator element e of tile (i, j) is C[row][col] with
   // row = 8 * (e / 4) + 4 * (lane / 32) + e % 4, col = lane % 32.
   if (p.epi != kEpiElem) {
-    // Staged: the wavefront writes its WM x WC block (fp32) to LDS rows, then
-    // each lane reads OE consecutive values of a row, adds the residual in
-    // fp32 and stores them as one 16-byte vector.  With the SwiGLU pairing,
-    // tiles 2k and 2k+1 of the wavefront hold gate and up for the same 32
-    // output columns (the weight rows are interleaved in groups of 32), and
-    // the block written is silu(bf16(gate)) * bf16(up): the values a gate and
-    // an up GEMM with bf16 outputs would hand the SwiGLU kernel.
+    // Staged: the wavefront writes RP rows of its WM x WC block (fp32) to its
+    // own LDS rows, then each lane reads OE consecutive values of a row, adds
+    // the residual in fp32 and stores them as one 16-byte vector; WM / RP
+    // passes.  With the SwiGLU pairing, tiles 2k and 2k+1 of the wavefront
+    // hold gate and up for the same 32 output columns (the weight rows are
+    // interleaved in groups of 32), and the block written is
+    // silu(bf16(gate)) * bf16(up): the values a gate and an up GEMM with bf16
+    // outputs would hand the SwiGLU kernel.
     constexpr int OE = 16 / sizeof(TO);  // output elements per 16-byte store
     constexpr int WC_MAX = WN;           // staged columns per wavefront (SwiGLU: WN / 2)
     constexpr int PITCH = WC_MAX + 4;    // staged row pitch, floats
-    static_assert(4 * WM * PITCH * 4 <= NS * STAGE, "the staged tile fits the stages");
+    constexpr int RP = NW * WM * PITCH * 4 <= NS * STAGE ? WM : 32;  // rows per pass
+    constexpr int TP = RP / 32;                                       // tiles per pass
+    static_assert(NW * RP * PITCH * 4 <= NS * STAGE, "the staged rows fit the stages");
     __syncthreads();  // every wavefront is done with the stages
-    float* stg = reinterpret_cast<float*>(lds) + wid * (WM * PITCH);
+    float* stg = reinterpret_cast<float*>(lds) + wid * (RP * PITCH);
     const bool sw = p.epi == kEpiSwiglu;
     const int wc = sw ? WN / 2 : WN;
-    if (sw) {
-      static_assert(TN % 2 == 0 || TN == 1, "gate/up tiles come in pairs");
-      if constexpr (TN % 2 == 0) {
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int k = 0; k < TN / 2; ++k)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-              const float g = to_f32<bf16>((bf16)acc[i][2 * k][e]);
-              const float u = to_f32<bf16>((bf16)acc[i][2 * k + 1][e]);
-              stg[(i * 32 + 8 * (e / 4) + 4 * lg + (e % 4)) * PITCH + k * 32 + lr] = silu(g) * u;
-            }
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) stg[(i * 32 + 8 * (e / 4) + 4 * lg + (e % 4)) * PITCH + j * 32 + lr] = acc[i][j][e];
-    }
     // Rows of the block go to rows m0 + wm WM ..; columns to c0 ...
     const int c0 = sw ? (n0 + wn * WN) / 2 : n0 + wn * WN;
     const int ncols = sw ? p.N / 2 : p.N;
     const int cpr = wc / OE;  // 16-byte chunks per staged row
+#pragma unroll
+    for (int ip = 0; ip < TM / TP; ++ip) {
+      if (sw) {
+        static_assert(TN % 2 == 0 || TN == 1, "gate/up tiles come in pairs");
+        if constexpr (TN % 2 == 0) {
+#pragma unroll
+          for (int t = 0; t < TP; ++t)
+#pragma unroll
+            for (int k = 0; k < TN / 2; ++k)
+#pragma unroll
+              for (int e = 0; e < 16; ++e) {
+                const float g = to_f32<bf16>((bf16)acc[ip * TP + t][2 * k][e]);
+                const float u = to_f32<bf16>((bf16)acc[ip * TP + t][2 * k + 1][e]);
+                stg[(t * 32 + 8 * (e / 4) + 4 * lg + (e % 4)) * PITCH + k * 32 + lr] = silu(g) * u;
+              }
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < TP; ++t)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+              stg[(t * 32 + 8 * (e / 4) + 4 * lg + (e % 4)) * PITCH + j * 32 + lr] = acc[ip * TP + t][j][e];
+      }
 #pragma unroll 4
-    for (int c = lane; c < WM * cpr; c += 64) {
-      const int rl = c / cpr, cl = (c % cpr) * OE;
-      const int row = m0 + wm * WM + rl, col = c0 + cl;
-      if (row < p.M && col < ncols) {
-        float v[OE];
+      for (int c = lane; c < RP * cpr; c += 64) {
+        const int rl = c / cpr, cl = (c % cpr) * OE;
+        const int row = m0 + wm * WM + ip * RP + rl, col = c0 + cl;
+        if (row < p.M && col < ncols) {
+          float v[OE];
 #pragma unroll
-        for (int e = 0; e < OE; e += 4) {
-          const float4 x = *reinterpret_cast<const float4*>(stg + rl * PITCH + cl + e);
-          v[e] = x.x;
-          v[e + 1] = x.y;
-          v[e + 2] = x.z;
-          v[e + 3] = x.w;
-        }
-        if (R) {
-          float r[OE];
-          load16(R + (long)row * p.ldr + col, r);
+          for (int e = 0; e < OE; e += 4) {
+            const float4 x = *reinterpret_cast<const float4*>(stg + rl * PITCH + cl + e);
+            v[e] = x.x;
+            v[e + 1] = x.y;
+            v[e + 2] = x.z;
+            v[e + 3] = x.w;
+          }
+          if (R) {
+            float r[OE];
+            load16(R + (long)row * p.ldr + col, r);
 #pragma unroll
-          for (int e = 0; e < OE; ++e) v[e] += r[e];
+            for (int e = 0; e < OE; ++e) v[e] += r[e];
+          }
+          store_vec<OE>(C + (long)row * p.ldc + col, v);
         }
-        store_vec<OE>(C + (long)row * p.ldc + col, v);
       }
     }
     return;
@@ -547,6 +600,62 @@ static bool staged_ok(const GemmArgs& a) {
   return c_ok && r_ok;
 }
 
+// Tiles of the LDS-DMA kernel.
+enum DmaTile { kT64x64, kT64x128, kT128x128, kT128x256, kT256x128, kT256x256, kTileCount };
+
+template <typename TO, bool BT>
+static void launch_dma(DmaTile t, const GemmArgs& g, int batch, hipStream_t st) {
+  auto grid = [&](int bm, int bn) {
+    return dim3((unsigned)((long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn)), 1, (unsigned)batch);
+  };
+  switch (t) {
+    case kT256x256: gemm_dma_kernel<TO, 256, 256, BT, 2, 2, 4><<<grid(256, 256), dim3(512), 0, st>>>(g); break;
+    case kT256x128: gemm_dma_kernel<TO, 256, 128, BT, 3, 4, 2><<<grid(256, 128), dim3(512), 0, st>>>(g); break;
+    case kT128x256: gemm_dma_kernel<TO, 128, 256, BT, 3, 2, 4><<<grid(128, 256), dim3(512), 0, st>>>(g); break;
+    case kT128x128: gemm_dma_kernel<TO, 128, 128, BT, 4><<<grid(128, 128), dim3(256), 0, st>>>(g); break;
+    case kT64x128: gemm_dma_kernel<TO, 64, 128, BT, 6><<<grid(64, 128), dim3(256), 0, st>>>(g); break;
+    default: gemm_dma_kernel<TO, 64, 64, BT, 8><<<grid(64, 64), dim3(256), 0, st>>>(g); break;
+  }
+}
+
+// NKL_GEMM_TILE=64x64|64x128|128x128|128x256|256x128|256x256 forces a tile
+// (for measurements); -1 when unset or unknown.
+static int forced_tile() {
+  static const int forced = [] {
+    const char* f = getenv("NKL_GEMM_TILE");
+    if (!f) return -1;
+    static const char* names[kTileCount] = {"64x64", "64x128", "128x128", "128x256", "256x128", "256x256"};
+    for (int i = 0; i < kTileCount; ++i)
+      if (!strcmp(f, names[i])) return i;
+    return -1;
+  }();
+  return forced;
+}
+
+static long tiles_of(const GemmArgs& a, int bm, int bn, int batch) {
+  return (long)((a.M + bm - 1) / bm) * ((a.N + bn - 1) / bn) * batch;
+}
+
+// Tile choice.  With a 128x128 tile or larger for every CU, the tile whose
+// rounds of 256 workgroups (one per CU) cost least, at the time per K-step
+// of a round measured on MI355X (bf16, K-contiguous B): 256x256 1.85 us,
+// 256x128 1.25 us, 128x128 0.8 us.  Smaller GEMMs: the largest tile that
+// still gives every CU a workgroup.
+static DmaTile choose_tile(const GemmArgs& a, int batch) {
+  if (forced_tile() >= 0) return (DmaTile)forced_tile();
+  const long t128 = tiles_of(a, 128, 128, batch);
+  if (t128 >= 256) {
+    auto rounds = [](long t) { return (double)((t + 255) / 256); };
+    const double c256 = 1.85 * rounds(tiles_of(a, 256, 256, batch));
+    const double c256x128 = 1.25 * rounds(tiles_of(a, 256, 128, batch));
+    const double c128 = 0.8 * rounds(t128);
+    if (c256 <= c256x128 && c256 <= c128) return kT256x256;
+    return c256x128 < c128 ? kT256x128 : kT128x128;
+  }
+  if (tiles_of(a, 64, 128, batch) >= 256) return kT64x128;
+  return kT64x64;
+}
+
 template <typename T, typename TO, bool BT>
 static int gemm_dispatch(const GemmArgs& a, int batch, int variant, hipStream_t st) {
   constexpr int E = VecE<T>::value;
@@ -557,7 +666,6 @@ static int gemm_dispatch(const GemmArgs& a, int batch, int variant, hipStream_t 
     gemm_naive_kernel<T, TO, BT><<<dim3((unsigned)((tiles + 3) / 4), 1, batch), dim3(256), 0, st>>>(a);
     return check_launch("nkl_gemm(naive)");
   }
-  // Largest tile that still gives every CU a workgroup; 64x64 otherwise.
   const long t128 = (long)((a.M + 127) / 128) * ((a.N + 127) / 128) * batch;
   const long t64x128 = (long)((a.M + 63) / 64) * ((a.N + 127) / 128) * batch;
   if constexpr (std::is_same<T, bf16>::value) {
@@ -567,16 +675,7 @@ static int gemm_dispatch(const GemmArgs& a, int batch, int variant, hipStream_t 
     if (a_bytes < (1L << 31) && b_bytes < (1L << 31)) {
       GemmArgs g = a;
       g.epi = staged_ok<TO>(a) ? kEpiStaged : kEpiElem;
-      if (t128 >= 256) {
-        const long tiles = (long)((a.M + 127) / 128) * ((a.N + 127) / 128);
-        gemm_dma_kernel<TO, 128, 128, BT, 4><<<dim3((unsigned)tiles, 1, batch), dim3(256), 0, st>>>(g);
-      } else if (t64x128 >= 256) {
-        const long tiles = (long)((a.M + 63) / 64) * ((a.N + 127) / 128);
-        gemm_dma_kernel<TO, 64, 128, BT, 6><<<dim3((unsigned)tiles, 1, batch), dim3(256), 0, st>>>(g);
-      } else {
-        const long tiles = (long)((a.M + 63) / 64) * ((a.N + 63) / 64);
-        gemm_dma_kernel<TO, 64, 64, BT, 8><<<dim3((unsigned)tiles, 1, batch), dim3(256), 0, st>>>(g);
-      }
+      launch_dma<TO, BT>(choose_tile(a, batch), g, batch, st);
       return check_launch("nkl_gemm(blocked)");
     }
   }
@@ -642,14 +741,10 @@ extern "C" int nkl_gemm_swiglu(const void* A, const void* Bgu, void* C, int M, i
     return set_error(NKL_EINVAL, "nkl_gemm_swiglu: operands must be under 2 GiB");
   GemmArgs a{A, Bgu, C, nullptr, M, 2 * N, K, lda, ldb, ldc, 0, 0, 0, 0, 0, kEpiSwiglu};
   hipStream_t st = (hipStream_t)stream;
-  // Tiles 128 columns wide: each wavefront's 64 columns are one gate/up pair.
-  const long t128 = (long)((M + 127) / 128) * ((2L * N + 127) / 128);
-  if (t128 >= 256) {
-    gemm_dma_kernel<bf16, 128, 128, true, 4><<<dim3((unsigned)t128), dim3(256), 0, st>>>(a);
-  } else {
-    const long tiles = (long)((M + 63) / 64) * ((2L * N + 127) / 128);
-    gemm_dma_kernel<bf16, 64, 128, true, 6><<<dim3((unsigned)tiles), dim3(256), 0, st>>>(a);
-  }
+  // Every tile but 64x64 gives each wavefront 64 columns: one gate/up pair.
+  DmaTile t = choose_tile(a, 1);
+  if (t == kT64x64) t = kT64x128;
+  launch_dma<bf16, true>(t, a, 1, st);
   return check_launch("nkl_gemm_swiglu");
 }
 
