@@ -368,27 +368,30 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_dma_kernel(GemmArgs p) {
       boff[u] = col < cols_b ? (unsigned)(2 * ((long)row * p.ldb + col)) : kOOB;
     }
   }
-  // Copies K-step s into stage st (K-steps past K copy zeros).
-  auto dma = [&](int s, int st) __attribute__((always_inline)) {
+  // Copy instruction u (A for u < A_PW, then B) of K-step s into stage st
+  // (K-steps past K copy zeros).
+  auto dma1 = [&](int s, int st, int u) __attribute__((always_inline)) {
     const int k0 = s * G_BK;
     unsigned char* sb = lds + st * STAGE;
-#pragma unroll
-    for (int u = 0; u < A_PW; ++u) {
+    if (u < A_PW) {
       const unsigned off = (aoff[u] != kOOB && k0 + akc[u] < K) ? aoff[u] + 2u * k0 : kOOB;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (__attribute__((address_space(3))) void*)(sb + (wid * A_PW + u) * 1024),
                                                16, (int)off, 0, 0, 0);
-    }
-#pragma unroll
-    for (int u = 0; u < B_PW; ++u) {
+    } else {
+      const int w = u - A_PW;
       unsigned off;
       if constexpr (BT)
-        off = (boff[u] != kOOB && k0 + bkc[u] < K) ? boff[u] + 2u * k0 : kOOB;
+        off = (boff[w] != kOOB && k0 + bkc[w] < K) ? boff[w] + 2u * k0 : kOOB;
       else
-        off = (boff[u] != kOOB && k0 + brow[u] < K) ? boff[u] + (unsigned)(2L * k0 * p.ldb) : kOOB;
+        off = (boff[w] != kOOB && k0 + brow[w] < K) ? boff[w] + (unsigned)(2L * k0 * p.ldb) : kOOB;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rb, (__attribute__((address_space(3))) void*)(sb + A_BYTES + (wid * B_PW + u) * 1024), 16, (int)off, 0, 0,
+          rb, (__attribute__((address_space(3))) void*)(sb + A_BYTES + (wid * B_PW + w) * 1024), 16, (int)off, 0, 0,
           0);
     }
+  };
+  auto dma = [&](int s, int st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) dma1(s, st, u);
   };
 
   // ---- fragment offsets within a stage (K-step sub-step ks = 0..3)
@@ -486,11 +489,20 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_dma_kernel(GemmArgs p) {
     g_wait_vm<(NS - 2) * LPT>();  // K-step s+1 has landed
     g_wait_lgkm0();               // this wavefront's reads of K-step s are done
     barrier();                    // ... for every wavefront
-    dma(s + NS, s % NS);          // into K-step s's stage
+    // The last sub-step's MFMAs (fragments already in registers) go out
+    // interleaved with the next K-step's first fragment reads and the copies
+    // into K-step s's stage: a burst of LPT copies would hold the wavefront's
+    // issue while the address unit drains them.  The reads come first in
+    // program order (the copies may alias them).
     frags(lds + ((s + 1) % NS) * STAGE, 0, fa[0], fb[0]);
-    __builtin_amdgcn_sched_barrier(0);
-    mmas(fa[1], fb[1]);
-    __builtin_amdgcn_sched_barrier(0);
+    constexpr int NMMA = TM * TN, PER = (LPT + NMMA - 1) / NMMA;  // copies per MFMA
+#pragma unroll
+    for (int k = 0; k < NMMA; ++k) {
+      acc[k / TN][k % TN] = MF::mma(fa[1][k / TN], fb[1][k % TN], acc[k / TN][k % TN]);
+#pragma unroll
+      for (int u = k * PER; u < (k + 1) * PER && u < LPT; ++u) dma1(s + NS, s % NS, u);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
   __builtin_amdgcn_s_waitcnt(0);  // the copies of K-steps past K have landed
 
