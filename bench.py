@@ -146,6 +146,47 @@ def bench_matmul(reps, warmup):
             "frac": flops / sec / 1e12 / PEAK_BF16_TFLOPS}
 
 
+# The decoder block's GEMMs (hidden 2048, 16 heads, FFN 5632, 2048 tokens) and
+# two square ones, as (M, N, K, B layout): "nt" is B given [N, K] (a Linear
+# weight), "nn" B given [K, N].
+GEMM_SHAPES = [(1024, 1024, 1024, "nn"), (2048, 6144, 2048, "nt"), (2048, 2048, 2048, "nt"),
+               (2048, 11264, 2048, "nt"), (2048, 2048, 5632, "nt"), (4096, 4096, 4096, "nt")]
+
+
+def bench_gemm_shapes(reps, warmup):
+    """nkl_gemm (its own tile choice) beside torch.mm (hipBLASLt) on the same
+    rotating bf16 operands: library context for the hand-written kernel."""
+    import torch
+
+    from nkilab import ops
+
+    out = {}
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    for M, N, K, kind in GEMM_SHAPES:
+        per_set = 2 * (M * K + N * K + 2 * M * N)
+        sets = []
+        for _ in range(min(n_sets(per_set), 8)):
+            a = torch.randn(M, K, device="cuda", generator=gen).to(torch.bfloat16)
+            b = torch.randn(*((K, N) if kind == "nn" else (N, K)), device="cuda", generator=gen).to(torch.bfloat16)
+            sets.append((a, b, torch.empty(M, N, device="cuda", dtype=torch.bfloat16),
+                         torch.empty(M, N, device="cuda", dtype=torch.bfloat16)))
+        if kind == "nn":
+            ours = [lambda t=t: ops.gemm_into(t[0], t[1], t[2]) for t in sets]
+            lib = [lambda t=t: torch.mm(t[0], t[1], out=t[3]) for t in sets]
+        else:
+            ours = [lambda t=t: ops.linear_into(t[0], t[1], t[2]) for t in sets]
+            lib = [lambda t=t: torch.mm(t[0], t[1].t(), out=t[3]) for t in sets]
+        s_ours, s_lib = time_launches(ours, reps, warmup), time_launches(lib, reps, warmup)
+        flops = 2 * M * N * K
+        out[f"{M}x{N}x{K}_{kind}"] = {
+            "us": round(s_ours * 1e6, 3), "tflops": round(flops / s_ours / 1e12, 1),
+            "frac": round(flops / s_ours / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "torch_mm_us": round(s_lib * 1e6, 3), "torch_mm_tflops": round(flops / s_lib / 1e12, 1),
+            "max_abs_diff_vs_torch": float((sets[0][2].float() - sets[0][3].float()).abs().max())}
+        del sets
+    return out
+
+
 def bench_decoder(reps, warmup):
     import torch
 
@@ -357,6 +398,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--all", action="store_true", help="also the GEMM, long-context and decoder configs")
+    ap.add_argument("--gemm-shapes", action="store_true", help="only the GEMM shapes beside torch.mm, one JSON line")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--report", default=None, help="write the full result dict as JSON here")
     ap.add_argument("--pmc-pass", action="store_true", help="eager launches for a rocprofv3 --pmc run, no timing")
@@ -387,6 +429,9 @@ def main() -> int:
         return 0
     props = torch.cuda.get_device_properties(0)
     log(f"device: {props.name} CUs={props.multi_processor_count} lib={_lib.LIB_PATH}")
+    if args.gemm_shapes:
+        print(json.dumps({"gemm_shapes": bench_gemm_shapes(args.steps, args.warmup)}), flush=True)
+        return 0
 
     A = dict(H=8, S=2048, d=128)
     log(f"attention {A} ...")
@@ -424,6 +469,8 @@ def main() -> int:
                 "frac": r["tflops"] / PEAK_BF16_TFLOPS}
         log("decoder block ...")
         result["decoder_block"] = bench_decoder(max(3, args.steps // 10), 2)
+        log("GEMM shapes (nkl_gemm and torch.mm) ...")
+        result["gemm_shapes"] = bench_gemm_shapes(max(3, args.steps // 5), 2)
     if not args.no_cpu:
         log("CPU baseline ...")
         q, k, v, o = bufs

@@ -534,8 +534,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_dma_kernel(GemmArgs p) {
 #pragma unroll
     for (int ip = 0; ip < TM / TP; ++ip) {
       if (sw) {
-        static_assert(TN % 2 == 0 || TN == 1, "gate/up tiles come in pairs");
-        if constexpr (TN % 2 == 0) {
+        if constexpr (TN % 2 == 0) {  // gate/up tiles come in pairs (the host picks such a tile)
 #pragma unroll
           for (int t = 0; t < TP; ++t)
 #pragma unroll
@@ -613,7 +612,7 @@ static bool staged_ok(const GemmArgs& a) {
 }
 
 // Tiles of the LDS-DMA kernel.
-enum DmaTile { kT64x64, kT64x128, kT128x128, kT128x256, kT256x128, kT256x256, kTileCount };
+enum DmaTile { kT64x64, kT64x128, kT128x128, kT128x256, kT256x128, kT256x192, kT256x256, kTileCount };
 
 template <typename TO, bool BT>
 static void launch_dma(DmaTile t, const GemmArgs& g, int batch, hipStream_t st) {
@@ -622,6 +621,7 @@ static void launch_dma(DmaTile t, const GemmArgs& g, int batch, hipStream_t st) 
   };
   switch (t) {
     case kT256x256: gemm_dma_kernel<TO, 256, 256, BT, 2, 2, 4><<<grid(256, 256), dim3(512), 0, st>>>(g); break;
+    case kT256x192: gemm_dma_kernel<TO, 256, 192, BT, 2, 4, 2><<<grid(256, 192), dim3(512), 0, st>>>(g); break;
     case kT256x128: gemm_dma_kernel<TO, 256, 128, BT, 3, 4, 2><<<grid(256, 128), dim3(512), 0, st>>>(g); break;
     case kT128x256: gemm_dma_kernel<TO, 128, 256, BT, 3, 2, 4><<<grid(128, 256), dim3(512), 0, st>>>(g); break;
     case kT128x128: gemm_dma_kernel<TO, 128, 128, BT, 4><<<grid(128, 128), dim3(256), 0, st>>>(g); break;
@@ -636,7 +636,7 @@ static int forced_tile() {
   static const int forced = [] {
     const char* f = getenv("NKL_GEMM_TILE");
     if (!f) return -1;
-    static const char* names[kTileCount] = {"64x64", "64x128", "128x128", "128x256", "256x128", "256x256"};
+    static const char* names[kTileCount] = {"64x64", "64x128", "128x128", "128x256", "256x128", "256x192", "256x256"};
     for (int i = 0; i < kTileCount; ++i)
       if (!strcmp(f, names[i])) return i;
     return -1;
@@ -650,19 +650,25 @@ static long tiles_of(const GemmArgs& a, int bm, int bn, int batch) {
 
 // Tile choice.  With a 128x128 tile or larger for every CU, the tile whose
 // rounds of 256 workgroups (one per CU) cost least, at the time per K-step
-// of a round measured on MI355X (bf16, K-contiguous B): 256x256 1.85 us,
-// 256x128 1.25 us, 128x128 0.8 us.  Smaller GEMMs: the largest tile that
-// still gives every CU a workgroup.
+// of a round measured on MI355X (bf16, K-contiguous B): 256x256 1.9 us,
+// 256x192 1.75 us, 256x128 1.25 us, 128x128 0.8 us.  256x192 fills the CUs
+// where 256x256 leaves a quarter idle (2048 x 6144: 256 tiles against 192).
+// Smaller GEMMs: the largest tile that still gives every CU a workgroup.
 static DmaTile choose_tile(const GemmArgs& a, int batch) {
   if (forced_tile() >= 0) return (DmaTile)forced_tile();
   const long t128 = tiles_of(a, 128, 128, batch);
   if (t128 >= 256) {
     auto rounds = [](long t) { return (double)((t + 255) / 256); };
-    const double c256 = 1.85 * rounds(tiles_of(a, 256, 256, batch));
-    const double c256x128 = 1.25 * rounds(tiles_of(a, 256, 128, batch));
-    const double c128 = 0.8 * rounds(t128);
-    if (c256 <= c256x128 && c256 <= c128) return kT256x256;
-    return c256x128 < c128 ? kT256x128 : kT128x128;
+    const struct { DmaTile t; double c; } cand[] = {
+        {kT256x256, 1.9 * rounds(tiles_of(a, 256, 256, batch))},
+        {kT256x192, 1.75 * rounds(tiles_of(a, 256, 192, batch))},
+        {kT256x128, 1.25 * rounds(tiles_of(a, 256, 128, batch))},
+        {kT128x128, 0.8 * rounds(t128)}};
+    DmaTile best = kT256x256;
+    double cb = 1e30;
+    for (const auto& c : cand)
+      if (c.c < cb) cb = c.c, best = c.t;
+    return best;
   }
   if (tiles_of(a, 64, 128, batch) >= 256) return kT64x128;
   return kT64x64;
@@ -753,9 +759,10 @@ extern "C" int nkl_gemm_swiglu(const void* A, const void* Bgu, void* C, int M, i
     return set_error(NKL_EINVAL, "nkl_gemm_swiglu: operands must be under 2 GiB");
   GemmArgs a{A, Bgu, C, nullptr, M, 2 * N, K, lda, ldb, ldc, 0, 0, 0, 0, 0, kEpiSwiglu};
   hipStream_t st = (hipStream_t)stream;
-  // Every tile but 64x64 gives each wavefront 64 columns: one gate/up pair.
+  // A tile whose wavefronts own 64 columns: one gate/up pair.
   DmaTile t = choose_tile(a, 1);
   if (t == kT64x64) t = kT64x128;
+  if (t == kT256x192) t = kT256x256;
   launch_dma<bf16, true>(t, a, 1, st);
   return check_launch("nkl_gemm_swiglu");
 }

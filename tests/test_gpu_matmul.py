@@ -140,6 +140,36 @@ def test_staged_epilogue_matches_element_epilogue(rng, M, K, N, out_dt, res):
     assert rel_err(_np(c), ref) < (1e-5 if out_dt == torch.float32 else 1e-2)
 
 
+# Shapes the tile choice sends to 256x192, 256x256, 256x128 and 128x128 (in
+# that order; rounds of 256 workgroups x measured cost per K-step), each with
+# partial tiles at both edges of C.
+@pytest.mark.parametrize("M,K,N", [(2000, 136, 6104), (4000, 136, 4000), (2040, 136, 4088), (2000, 200, 2000)])
+@pytest.mark.parametrize("layout", ["nt", "nn"])
+def test_large_tile_gemms_with_ragged_edges(rng, M, K, N, layout):
+    """bf16 GEMMs on the large tiles against a float64 product; the staged
+    epilogue (aligned C) and the element epilogue (C one element off) agree
+    exactly, residual included."""
+    from nkilab import ops
+
+    a = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).to(torch.bfloat16).cuda()
+    b = torch.from_numpy(rng.standard_normal((N, K) if layout == "nt" else (K, N)).astype(np.float32))
+    b = b.to(torch.bfloat16).cuda()
+    r = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float32)).to(torch.bfloat16).cuda()
+    run = (lambda c: ops.linear_into(a, b, c, residual=r)) if layout == "nt" else \
+        (lambda c: ops.gemm_into(a, b, c, residual=r))
+    c = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    run(c)
+    big = torch.empty((M, N + 1), dtype=torch.bfloat16, device="cuda")
+    run(big[:, 1:])
+    assert torch.equal(c, big[:, 1:])
+    bt = b.double().cpu() if layout == "nn" else b.double().cpu().t()
+    ref = (a.double().cpu() @ bt + r.double().cpu()).numpy()
+    assert rel_err(_np(c), ref) < 1e-2
+    # one rounding of the fp32 sum: within one bf16 ulp of the exact value, plus
+    # the fp32 accumulation error (~K * 2^-24 * |terms|) where C is near zero
+    assert_within_bf16_ulps(_np(c), ref, 1, floor=2e-3)
+
+
 @pytest.mark.parametrize("M,K,N", [(2048, 2048, 5632), (300, 256, 96), (64, 128, 32), (1, 64, 64), (513, 384, 704)])
 def test_gemm_swiglu_equals_gate_up_then_swiglu(rng, M, K, N):
     """The fused gate/up GEMM with SwiGLU in its epilogue is bit-identical to
