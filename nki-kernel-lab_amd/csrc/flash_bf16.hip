@@ -385,6 +385,21 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
       }
     }
 
+    // ---- the next segment of the range: its Q and first K/V tile are loaded
+    // as soon as the loop is done with Q and the staging registers, so that
+    // their latency overlaps the hand-over between the teams and the stores
+    // of this segment (issued after the stores they would wait for them too:
+    // loads and stores share the vector memory counter).
+    const long next_u = bstart + t1;
+    const bool more = next_u < u1;
+    Seg nxt = cur;
+    if (more) nxt = decode(next_u);
+    if (more) {
+      load_q(nxt, qf);  // this segment's Q fragments are no longer needed
+      gload(nxt, 0, p.k, p.k_sh, p.k_ss, goff_k, rk);
+      gload(nxt, 0, p.v, p.v_sh, p.v_ss, goff_v, rv);
+    }
+
     // ---- hand-over between the teams.  Team t finishes d-blocks
     // [t OWN, (t + 1) OWN) of O (teams past the last d-block finish none) and
     // writes the other d-blocks of its state, with its (m, l), to LDS.  A
@@ -501,29 +516,12 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
       }
     };
 
-    // ---- the next segment of the range: its Q and first K/V tile are loaded
-    // before this segment's results are stored.  Loads and stores share the
-    // vector memory counter, so a load issued after the stores is held until
-    // the stores complete; issued first, their latencies overlap.
-    const long next_u = bstart + t1;
-    const bool more = next_u < u1;
-    Seg nxt = cur;
-    if (more) nxt = decode(next_u);
-    auto prefetch = [&]() __attribute__((always_inline)) {
-      if (more) {
-        load_q(nxt, qf);  // this segment's Q fragments are no longer needed
-        gload(nxt, 0, p.k, p.k_sh, p.k_ss, goff_k, rk);
-        gload(nxt, 0, p.v, p.v_sh, p.v_ss, goff_v, rv);
-      }
-    };
-
     // ---- finish the query block, or hand a partial state to the last arriver
     int nparts = 1, vf = vidx;
     if (w.sched == kBalanced) {
       vf = range_of(bstart, w);
       nparts = range_of(bstart + nt_b - 1, w) - vf + 1;
     }
-    prefetch();  // one definition of the next segment's registers for both paths (no copies, no wait)
     if (nparts == 1) {
       store_out();
     } else {
