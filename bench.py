@@ -132,6 +132,26 @@ def bench_rows(R, D, reps, warmup, seed=0):
     return out
 
 
+def bench_copy_ceiling(R, D, reps, warmup):
+    """The HBM ceiling at the row kernels' size: nkl_stream_copy of one
+    [R, D] bf16 tensor (their access pattern, no arithmetic), same harness."""
+    import torch
+
+    from nkilab import _lib
+    from nkilab._tensors import stream_handle
+
+    x = torch.empty((R, D), dtype=torch.bfloat16, device="cuda").normal_()
+    nb = x.numel() * 2
+    sets = n_sets(2 * nb)
+    bufs = [(x.clone(), torch.empty_like(x)) for _ in range(sets)]
+    sec = time_launches([lambda b=b: _lib.call("nkl_stream_copy", b[0].data_ptr(), b[1].data_ptr(), nb,
+                                                stream_handle()) for b in bufs], reps, warmup)
+    ok = all(torch.equal(a, b) for a, b in bufs)
+    del bufs
+    return {"us": sec * 1e6, "GB/s": 2 * nb / sec / 1e9, "frac": 2 * nb / sec / 1e9 / PEAK_HBM_GBS,
+            "bytes": 2 * nb, "buffer_sets": sets, "copy_exact": ok}
+
+
 def bench_matmul(reps, warmup):
     import torch
 
@@ -441,6 +461,9 @@ def main() -> int:
     rows = bench_rows(4096, 2048, args.steps, args.warmup)
     for k, r in rows.items():
         log(f"  {k:8s} {r['us']:.2f} us  {r['GB/s']:.0f} GB/s  {100 * r['frac']:.1f}% of HBM peak")
+    copy = bench_copy_ceiling(4096, 2048, args.steps, args.warmup)
+    log(f"  copy     {copy['us']:.2f} us  {copy['GB/s']:.0f} GB/s  {100 * copy['frac']:.1f}% of HBM peak "
+        f"(the same 32 MiB of traffic, no arithmetic)")
 
     traffic = load_traffic()
     result = {
@@ -454,9 +477,12 @@ def main() -> int:
                    "device": props.name, "cus": props.multi_processor_count},
         "roofline": roofline("mfma", att["tflops"], "TFLOP/s", traffic.get("attention", {}).get("bytes")),
         "row_kernels": {k: {"us": round(r["us"], 3), "GB/s": round(r["GB/s"], 1), "frac": round(r["frac"], 4),
-                            "bytes": r["bytes"],
+                            "bytes": r["bytes"], "frac_of_copy_ceiling": round(r["GB/s"] / copy["GB/s"], 4),
                             "roofline": roofline("hbm", r["GB/s"], "GB/s", traffic.get(k, {}).get("bytes"))}
                         for k, r in rows.items()},
+        "hbm_copy_ceiling": {"us": round(copy["us"], 3), "GB/s": round(copy["GB/s"], 1),
+                             "frac": round(copy["frac"], 4), "bytes": copy["bytes"], "copy_exact": copy["copy_exact"],
+                             "kernel": "nkl_stream_copy: the row kernels' loads and non-temporal stores, no arithmetic"},
     }
     if args.all:
         log("matmul 1024^3 bf16 ...")

@@ -137,6 +137,15 @@ int nkl_swiglu(const void* g, const void* u, void* y, long n, int dtype,
                void* stream);
 
 /*
+ * y = x over nbytes (a multiple of 16; both pointers 16-byte aligned): the
+ * row kernels' access pattern (4 16-byte chunks in flight per lane, then
+ * non-temporal stores) with none of their arithmetic.  No counterpart in the
+ * reference: a measurement entry point that gives the HBM ceiling the row
+ * kernels' roofline is read against, at their size and in the same run.
+ */
+int nkl_stream_copy(const void* x, void* y, long nbytes, void* stream);
+
+/*
  * Causal attention O = softmax(Q K^T * scale + causal mask) V, flash style:
  * online softmax over key tiles, key tiles wholly above the diagonal are
  * skipped, the diagonal tiles are masked (key > query).

@@ -321,6 +321,26 @@ static int swiglu_launch(const void* g, const void* u, void* y, long n, hipStrea
   return check_launch("nkl_swiglu");
 }
 
+// Streaming copy with the row kernels' access pattern and none of their
+// arithmetic: each lane reads 4 16-byte chunks one grid span apart, then
+// writes them with non-temporal stores.  It measures the HBM ceiling the row
+// kernels' roofline is read against at the same size.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void stream_copy_kernel(const u32x4* __restrict__ x, u32x4* __restrict__ y, long n) {
+  const long base = (long)blockIdx.x * 256 + threadIdx.x, span = (long)gridDim.x * 256;
+  u32x4 v[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const long i = base + k * span;
+    v[k] = i < n ? x[i] : u32x4{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const long i = base + k * span;
+    if (i < n) __builtin_nontemporal_store(v[k], y + i);
+  }
+}
+
 }  // namespace nkl
 
 using namespace nkl;
@@ -400,4 +420,18 @@ extern "C" int nkl_swiglu(const void* g, const void* u, void* y, long n, int dty
   if (dtype == NKL_F32) return swiglu_launch<float>(g, u, y, n, st);
   if (dtype == NKL_BF16) return swiglu_launch<bf16>(g, u, y, n, st);
   return set_error(NKL_EDTYPE, "nkl_swiglu: unsupported dtype %d", dtype);
+}
+
+extern "C" int nkl_stream_copy(const void* x, void* y, long nbytes, void* stream) {
+  if (nbytes < 0 || nbytes % 16 != 0)
+    return set_error(NKL_EINVAL, "nkl_stream_copy: %ld bytes is not a non-negative multiple of 16", nbytes);
+  if (nbytes == 0) return NKL_OK;
+  if (!x || !y || ((uintptr_t)x & 15u) || ((uintptr_t)y & 15u))
+    return set_error(NKL_EINVAL, "nkl_stream_copy: null or non-16-byte-aligned pointer");
+  const long n = nbytes / 16;
+  const long grid = (n + 4 * 256 - 1) / (4 * 256);
+  if (grid > 0x7fffffffL) return set_error(NKL_EINVAL, "nkl_stream_copy: %ld bytes is too large", nbytes);
+  stream_copy_kernel<<<dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream>>>(static_cast<const u32x4*>(x),
+                                                                                   static_cast<u32x4*>(y), n);
+  return check_launch("nkl_stream_copy");
 }

@@ -209,3 +209,19 @@ def test_rope_in_place_on_strided_views(rng):
     ref = O.rope(before[:, :H * hd].view(S, H, hd).transpose(0, 1).cpu().numpy(), 0, 10000.0)
     assert np.abs(q.cpu().numpy() - ref).max() < 1e-4
     assert torch.equal(qkv[:, H * hd:], before[:, H * hd:])
+
+
+@pytest.mark.parametrize("nbytes", [16, 4096 * 2048 * 2, 16 * 1000 + 16 * 257, 16 * 1024 * 4 + 16])
+def test_stream_copy_is_exact(nbytes):
+    """The HBM-ceiling copy (measurement entry point): y == x byte for byte,
+    including sizes that leave a partial last workgroup; bytes past the end
+    stay untouched."""
+    from nkilab import _lib
+    from nkilab._tensors import stream_handle
+
+    x = torch.randint(0, 256, (nbytes + 64,), dtype=torch.uint8, device="cuda")
+    y = torch.full((nbytes + 64,), 7, dtype=torch.uint8, device="cuda")
+    _lib.call("nkl_stream_copy", x.data_ptr(), y.data_ptr(), nbytes, stream_handle())
+    torch.cuda.synchronize()
+    assert torch.equal(y[:nbytes], x[:nbytes])
+    assert bool((y[nbytes:] == 7).all())

@@ -45,6 +45,9 @@ def test_abi_rejects_bad_arguments_before_launching():
     assert L.nkl_softmax(None, None, 0, 16, 16, 16, 1, None) == 0  # empty: nothing to do
     assert L.nkl_softmax(None, None, 4, 16, 8, 16, 1, None) == -1  # ld < cols
     assert L.nkl_swiglu(None, None, None, -3, 0, None) == -1
+    assert L.nkl_stream_copy(None, None, 0, None) == 0  # empty: nothing to do
+    assert L.nkl_stream_copy(None, None, 24, None) == -1  # not a multiple of 16
+    assert L.nkl_stream_copy(None, None, 32, None) == -1  # null pointers
     assert L.nkl_rmsnorm(None, None, None, 4, 4, 4, 4, ctypes.c_float(1e-6), 1, 0, None) == -2  # bf16 -> f32
     assert L.nkl_flash_attn_causal(None, None, None, None, 1, 16, 256, 0, 0, 0, 0, 0, 0, 0, 0,
                                    ctypes.c_float(0.1), 1, None) == -1  # d > 128
