@@ -270,14 +270,48 @@ def cpu_baseline(q, k, v, gpu_out):
     except Exception:  # pragma: no cover
         model = "unknown"
     rows = cpu_rows_baseline(ncores)
+    other = cpu_gemm_decoder_baseline(ncores)
     base = {"value": round(flops / sec / 1e12, 5), "unit": "TFLOP/s", "cores": blas_threads, "kind": "port",
             "sample": f"full workload {H}x{S}x{d} bf16 values, oracle flash_pipelined (NumPy fp32, 128x128 tiles), "
                       f"mean of {reps} runs, {sec:.2f} s each",
             "cpu": model,
             "torch_cpu_sdpa_fp32": {"value": round(flops / tsec / 1e12, 5), "unit": "TFLOP/s", "cores": ncores,
                                     "sec": round(tsec, 4)},
-            "row_kernels": rows}
+            "row_kernels": rows, **other}
     return base, {"attention_rel_err_vs_oracle": parity, "attention_rel_err_vs_fp32_sdpa": sdpa_err}
+
+
+def cpu_gemm_decoder_baseline(ncores: int) -> dict:
+    """The 1024^3 matmul (the oracle's K-chunked NumPy restatement on one
+    BLAS pool, and torch.matmul in fp32 and bf16) and one forward of the fp32
+    DecoderBlock at the decoder config, on this host's cores."""
+    import torch
+
+    import oracle as O
+    from nkilab import workloads
+
+    a, b = workloads.matmul_inputs()
+    an, bn = a.float().numpy(), b.float().numpy()
+
+    def timed(fn, reps):
+        fn()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        return (time.perf_counter() - t0) / reps
+
+    mm_flops = 2 * 1024 ** 3
+    out = {"matmul_1024": {
+        "oracle_numpy": {"TFLOP/s": round(mm_flops / timed(lambda: O.ops_matmul(an, bn, "blocked", O.BF16), 2) / 1e12, 5)},
+        "torch_cpu_float32": {"TFLOP/s": round(mm_flops / timed(lambda: a.float() @ b.float(), 3) / 1e12, 5)},
+        "torch_cpu_bfloat16": {"TFLOP/s": round(mm_flops / timed(lambda: a @ b, 3) / 1e12, 5)},
+        "cores": ncores}}
+    block, x = workloads.decoder_inputs()
+    with torch.no_grad():
+        sec = timed(lambda: block(x), 1)
+    out["decoder_block"] = {"torch_cpu_float32": {"TFLOP/s": round(227_641_655_296 / sec / 1e12, 5), "sec": round(sec, 3)},
+                            "cores": ncores, "sample": "one forward of the fp32 DecoderBlock, S=2048, after one warm-up"}
+    return out
 
 
 def cpu_rows_baseline(ncores: int) -> dict:
