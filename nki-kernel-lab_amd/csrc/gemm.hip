@@ -1,7 +1,11 @@
 // GEMM: C = A . op(B) (+ R) on 32x32 MFMA tiles with fp32 accumulation.
 //
-// Blocked kernel (the hot path): a 256-thread workgroup owns a BM x BN tile
-// of C; its four wavefronts are laid out 2 x 2 and each owns a
+// bf16 operands take the LDS-DMA kernel further down (gemm_dma_kernel: the
+// hot path, tiles from 64x64 to 256x256).
+//
+// Register-staged blocked kernel (fp32 operands, and bf16 operands the DMA
+// kernel's buffer offsets cannot address): a 256-thread workgroup owns a
+// BM x BN tile of C; its four wavefronts are laid out 2 x 2 and each owns a
 // (BM/2) x (BN/2) sub-tile of 32x32 MFMA accumulators.  Per K step of BK
 // elements (64 bytes of each operand row) the workgroup stages an A tile
 // [BM][BK] and a B tile [BN][BK] in LDS, both K-contiguous so that every MFMA

@@ -200,3 +200,28 @@ def test_gemm_swiglu_rejects_bad_shapes():
     w = torch.zeros((2 * 48, 64), dtype=torch.bfloat16, device="cuda")
     with pytest.raises(ValueError, match="multiple of 32"):
         ops.gemm_swiglu_into(h, w, torch.empty((16, 48), dtype=torch.bfloat16, device="cuda"))
+
+
+@pytest.mark.parametrize("layout", ["nt", "nn"])
+def test_batched_gemm_on_large_tiles(rng, layout):
+    """Three independent products in one launch (blockIdx.z over the batch,
+    per-batch strides), a shape the tile choice sends to 256x128 and with
+    partial tiles at both edges: each batch entry against its own float64
+    product, residual included."""
+    from nkilab import _lib
+    from nkilab._tensors import stream_handle
+
+    B, M, N, K = 3, 1500, 1600, 136
+    a = torch.from_numpy(rng.standard_normal((B, M, K)).astype(np.float32)).to(torch.bfloat16).cuda()
+    bsh = (B, N, K) if layout == "nt" else (B, K, N)
+    b = torch.from_numpy(rng.standard_normal(bsh).astype(np.float32)).to(torch.bfloat16).cuda()
+    r = torch.from_numpy(rng.standard_normal((B, M, N)).astype(np.float32)).to(torch.bfloat16).cuda()
+    c = torch.empty((B, M, N), dtype=torch.bfloat16, device="cuda")
+    ldb = K if layout == "nt" else N
+    _lib.call("nkl_gemm", a.data_ptr(), b.data_ptr(), c.data_ptr(), r.data_ptr(), M, N, K, K, ldb, N, N,
+              1 if layout == "nt" else 0, B, M * K, bsh[1] * bsh[2], M * N, M * N, 1, 1, 0, stream_handle())
+    torch.cuda.synchronize()
+    for i in range(B):
+        bt = b[i].double().cpu() if layout == "nn" else b[i].double().cpu().t()
+        ref = (a[i].double().cpu() @ bt + r[i].double().cpu()).numpy()
+        assert_within_bf16_ulps(_np(c[i]), ref, 1, floor=2e-3)
