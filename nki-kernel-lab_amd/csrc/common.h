@@ -194,6 +194,33 @@ __device__ __forceinline__ float silu(float g) {
   return g * __builtin_amdgcn_rcpf(1.0f + fast_exp2(-g * kLog2e));
 }
 
+// ds_read_b64_tr_b16 through inline assembly, for kernels whose LDS is also
+// filled by LDS-DMA copies.  The compiler's builtin form of this read makes it
+// wait for every outstanding copy (vmcnt(0)) first, as it cannot tell the
+// copies' LDS ranges from the one read, which leaves only one stage of copies
+// in flight; the callers' protocols (each wavefront's vmcnt wait for its own
+// copies of a stage, then a barrier) already order the two.  The compiler does
+// not track this read's completion: its result goes through lds_wait_tie()
+// before any use.
+typedef short shortx4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ shortx4 ds_read_tr16_b64_async(const void* lds_ptr) {
+  shortx4 r;
+  const unsigned a = (unsigned)(size_t)(const __attribute__((address_space(3))) void*)lds_ptr;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(a));
+  return r;
+}
+// ds_read_b128 in the same untracked form (so that the compiler's lgkmcnt
+// waits for its own reads do not count across untracked ones).
+__device__ __forceinline__ bf16x8 ds_read_b128_async(const void* lds_ptr) {
+  bf16x8 r;
+  const unsigned a = (unsigned)(size_t)(const __attribute__((address_space(3))) void*)lds_ptr;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(a));
+  return r;
+}
+// Waits for every outstanding LDS read of this wavefront (lgkmcnt(0)) and
+// hands x on as the wait's output, so that no use of x precedes the wait.
+__device__ __forceinline__ void lds_wait_tie(bf16x8& x) { asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x)); }
+
 __device__ __forceinline__ bf16x8 load_frag(const bf16* p) {
   return *reinterpret_cast<const bf16x8*>(p);
 }

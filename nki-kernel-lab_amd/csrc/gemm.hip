@@ -436,17 +436,20 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_dma_kernel(GemmArgs p) {
   // Fragments of sub-step ks (16 K) of the stage at sb.
   auto frags = [&](const unsigned char* sb, int ks, bf16x8 (&af)[TM], bf16x8 (&bfr)[TN])
                    __attribute__((always_inline)) {
+    // With B as [K, N] every fragment read is untracked (see
+    // ds_read_tr16_b64_async); lds_wait_tie on the B fragments orders them all.
 #pragma unroll
-    for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const bf16x8*>(sb + afo[ks] + 4096 * i);
+    for (int i = 0; i < TM; ++i)
+      af[i] = BT ? *reinterpret_cast<const bf16x8*>(sb + afo[ks] + 4096 * i)
+                 : ds_read_b128_async(sb + afo[ks] + 4096 * i);
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       if constexpr (BT) {
         bfr[j] = *reinterpret_cast<const bf16x8*>(sb + bto[ks] + 4096 * j);
       } else {
-        typedef short shortx4 __attribute__((ext_vector_type(4)));
-        typedef __attribute__((address_space(3))) shortx4 lds_s4;
-        const shortx4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(sb + bfo[j][ks][0]));
-        const shortx4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(sb + bfo[j][ks][1]));
+        // (untracked reads: tied by lds_wait_tie before the MFMAs use them)
+        const shortx4 x = ds_read_tr16_b64_async(sb + bfo[j][ks][0]);
+        const shortx4 y = ds_read_tr16_b64_async(sb + bfo[j][ks][1]);
         bfr[j] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7));
       }
     }
@@ -470,13 +473,39 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_dma_kernel(GemmArgs p) {
   };
 
   // Software pipeline: the fragments of sub-step ks + 1 are read while the
-  // MFMAs of sub-step ks run; the stage hand-over (wait, barrier, next copy)
-  // sits between the reads and the MFMAs of the last sub-step, so the barrier
-  // wait overlaps MFMAs already issued.
+  // MFMAs of sub-step ks run; the stage hand-over (wait, barrier) sits between
+  // the reads and the MFMAs of the last sub-step, so the barrier wait overlaps
+  // MFMAs already issued.  The copies go out interleaved with MFMAs, never in
+  // a burst (each holds the wavefront's issue while the address unit drains
+  // it, ~35 cycles).  With three or more stages, the copies of K-step s+NS-1
+  // (into the stage freed at the end of step s-1) are spread over the four
+  // sub-steps of step s, NS-2 steps ahead of use; with two stages, the copies
+  // of K-step s+NS go out with the last sub-step, right after the barrier
+  // that frees their stage, one step ahead of use.
+  constexpr bool SPREAD = NS >= 3;
+  constexpr int NMMA = TM * TN;
+  constexpr int Q = (LPT + 3) / 4;  // copies per sub-step when spread
+  // Copies issued after K-step s+1's last one when step s waits for it: with
+  // SPREAD, K-steps s+2 .. s+NS-2 and the first 3 Q copies of K-step s+NS-1
+  // (its last ones go out after the wait); otherwise K-steps s+2 .. s+NS-1.
+  constexpr int WAITN = SPREAD ? (NS - 3) * LPT + 3 * Q : (NS - 2) * LPT;
+  static_assert(!SPREAD || 3 * Q <= LPT, "the last sub-step's share of the copies is not negative");
+  // The MFMAs of one sub-step with copies u0 .. u1-1 of K-step sd between them.
+  auto mma_copy = [&](const bf16x8 (&af)[TM], const bf16x8 (&bfr)[TN], int sd, int u0, int u1)
+                      __attribute__((always_inline)) {
+    const int per = (u1 - u0 + NMMA - 1) / NMMA;
+#pragma unroll
+    for (int k = 0; k < NMMA; ++k) {
+      acc[k / TN][k % TN] = MF::mma(af[k / TN], bfr[k % TN], acc[k / TN][k % TN]);
+#pragma unroll
+      for (int u = u0 + k * per; u < u0 + (k + 1) * per && u < u1; ++u) dma1(sd, sd % NS, u);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
   const int nk = (K + G_BK - 1) / G_BK;
 #pragma unroll
-  for (int s = 0; s < NS; ++s) dma(s, s);
-  g_wait_vm<(NS - 1) * LPT>();  // K-step 0 has landed
+  for (int s = 0; s < (SPREAD ? NS - 1 : NS); ++s) dma(s, s);
+  g_wait_vm<(SPREAD ? NS - 2 : NS - 1) * LPT>();  // K-step 0 has landed
   barrier();
   bf16x8 fa[2][TM], fb[2][TN];
   frags(lds, 0, fa[0], fb[0]);
@@ -485,28 +514,33 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_dma_kernel(GemmArgs p) {
     const unsigned char* sb = lds + (s % NS) * STAGE;
 #pragma unroll
     for (int ks = 0; ks < 3; ++ks) {
+      if constexpr (!BT) {  // B^T fragments of sub-step ks have landed (read one sub-step ago)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) lds_wait_tie(fb[ks & 1][j]);
+      }
       frags(sb, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
       __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of the MFMAs
-      mmas(fa[ks & 1], fb[ks & 1]);
+      if constexpr (SPREAD)
+        mma_copy(fa[ks & 1], fb[ks & 1], s + NS - 1, ks * Q, min((ks + 1) * Q, LPT));
+      else
+        mmas(fa[ks & 1], fb[ks & 1]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    g_wait_vm<(NS - 2) * LPT>();  // K-step s+1 has landed
-    g_wait_lgkm0();               // this wavefront's reads of K-step s are done
+    g_wait_vm<WAITN>();  // K-step s+1 has landed
+    g_wait_lgkm0();      // this wavefront's reads of K-step s are done
+    if constexpr (!BT) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) lds_wait_tie(fb[1][j]);
+    }
     barrier();                    // ... for every wavefront
-    // The last sub-step's MFMAs (fragments already in registers) go out
-    // interleaved with the next K-step's first fragment reads and the copies
-    // into K-step s's stage: a burst of LPT copies would hold the wavefront's
-    // issue while the address unit drains them.  The reads come first in
-    // program order (the copies may alias them).
+    // The next K-step's first fragment reads come first in program order
+    // (the copies may alias them), then the last sub-step's MFMAs, whose
+    // fragments are already in registers.
     frags(lds + ((s + 1) % NS) * STAGE, 0, fa[0], fb[0]);
-    constexpr int NMMA = TM * TN, PER = (LPT + NMMA - 1) / NMMA;  // copies per MFMA
-#pragma unroll
-    for (int k = 0; k < NMMA; ++k) {
-      acc[k / TN][k % TN] = MF::mma(fa[1][k / TN], fb[1][k % TN], acc[k / TN][k % TN]);
-#pragma unroll
-      for (int u = k * PER; u < (k + 1) * PER && u < LPT; ++u) dma1(s + NS, s % NS, u);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+    if constexpr (SPREAD)
+      mma_copy(fa[1], fb[1], s + NS - 1, 3 * Q, LPT);
+    else
+      mma_copy(fa[1], fb[1], s + NS, 0, LPT);  // into K-step s's stage
   }
   __builtin_amdgcn_s_waitcnt(0);  // the copies of K-steps past K have landed
 

@@ -142,8 +142,10 @@ def test_staged_epilogue_matches_element_epilogue(rng, M, K, N, out_dt, res):
 
 # Shapes the tile choice sends to 256x192, 256x256, 256x128 and 128x128 (in
 # that order; rounds of 256 workgroups x measured cost per K-step), each with
-# partial tiles at both edges of C.
-@pytest.mark.parametrize("M,K,N", [(2000, 136, 6104), (4000, 136, 4000), (2040, 136, 4088), (2000, 200, 2000)])
+# partial tiles at both edges of C; then long K-loops (hundreds of stage
+# hand-overs) on 128x128, 256x128 and 64x128.
+@pytest.mark.parametrize("M,K,N", [(2000, 136, 6104), (4000, 136, 4000), (2040, 136, 4088), (2000, 200, 2000),
+                                   (2000, 5632, 2000), (2040, 2056, 4088), (1000, 3000, 1000)])
 @pytest.mark.parametrize("layout", ["nt", "nn"])
 def test_large_tile_gemms_with_ragged_edges(rng, M, K, N, layout):
     """bf16 GEMMs on the large tiles against a float64 product; the staged
