@@ -217,6 +217,19 @@ __device__ __forceinline__ bf16x8 ds_read_b128_async(const void* lds_ptr) {
   asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(a));
   return r;
 }
+// The LDS byte address of p (a pointer into a __shared__ array), passed
+// through an empty asm: the compiler loses what it was computed from (a
+// wavefront-uniform value, kept in an SGPR).  Conversions between LDS
+// pointers and integers stay in device functions (a kernel body with them
+// lost its host launch stub).
+__device__ __forceinline__ unsigned opaque_lds_addr(const void* p) {
+  unsigned x = (unsigned)(size_t)(const __attribute__((address_space(3))) void*)p;
+  asm volatile("" : "+s"(x));
+  return x;
+}
+__device__ __forceinline__ __attribute__((address_space(3))) void* lds_ptr(unsigned a) {
+  return (__attribute__((address_space(3))) void*)(size_t)a;
+}
 // Waits for every outstanding LDS read of this wavefront (lgkmcnt(0)) and
 // hands x on as the wait's output, so that no use of x precedes the wait.
 __device__ __forceinline__ void lds_wait_tie(bf16x8& x) { asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x)); }

@@ -757,14 +757,16 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(static_cast<const bf16*>(p.v) + (long)(sg.hh / p.group) * p.v_sh + (long)k0 * p.v_ss), (short)0, vbytes,
         kBufferFlags);
-    unsigned char* sb = lds + st * W1_STAGEB;
+    // The stage's LDS address goes through an empty asm: with a destination
+    // it can see, the compiler makes every later LDS read wait for all
+    // outstanding copies (vmcnt(0)), which leaves one tile in flight; the
+    // per-stage vmcnt waits and the barrier order the copies and reads.
+    const unsigned sbase = opaque_lds_addr(lds + st * W1_STAGEB);
 #pragma unroll
     for (int u = 0; u < NI; ++u) {
       const int n = NI * wq + u;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(sb + n * 1024), 16,
-                                               dk[u], 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(sb + W1_TILEB + n * 1024),
-                                               16, dv[u], 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, lds_ptr(sbase + n * 1024), 16, dk[u], 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, lds_ptr(sbase + W1_TILEB + n * 1024), 16, dv[u], 0, 0, 0);
     }
   };
 
@@ -859,23 +861,31 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) pf[j] = (bf16)sc[8 * uu + j];
     };
+    // The V^T reads are untracked (ds_read_tr16_b64_async): the builtin
+    // transposed read would make the compiler wait for every outstanding copy
+    // first, leaving no tile in flight.  vties() orders them before P V.
     auto kfrags = [&](int st, bf16x8 (&kf)[NQF]) __attribute__((always_inline)) {
       const unsigned char* sb = lds + st * W1_STAGEB;
 #pragma unroll
       for (int f = 0; f < NQF; ++f) kf[f] = *reinterpret_cast<const bf16x8*>(sb + koff[f]);
     };
     auto vfrags = [&](int st, bf16x8 (&a)[NDB][2]) __attribute__((always_inline)) {
-      typedef short shortx4 __attribute__((ext_vector_type(4)));
-      typedef __attribute__((address_space(3))) shortx4 lds_s4;
       const unsigned char* sb = lds + st * W1_STAGEB;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int uu = 0; uu < 2; ++uu) {
-          const shortx4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(sb + voff[db][0] + 4096 * uu));
-          const shortx4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(sb + voff[db][1] + 4096 * uu));
+          const shortx4 x = ds_read_tr16_b64_async(sb + voff[db][0] + 4096 * uu);
+          const shortx4 y = ds_read_tr16_b64_async(sb + voff[db][1] + 4096 * uu);
           a[db][uu] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7));
         }
+    };
+    // Every LDS read so far has landed; P V uses the tied V^T fragments.
+    auto vties = [&](bf16x8 (&a)[NDB][2]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int uu = 0; uu < 2; ++uu) lds_wait_tie(a[db][uu]);
     };
 
     auto pv = [&](int hq, const bf16x8 (&va)[NDB][2], const bf16x8 (&pf)[2]) __attribute__((always_inline)) {
@@ -916,7 +926,12 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
       constexpr bool MSK = decltype(masked)::value;
       const int st1 = (st + 1) % W1_NS, stp = (st + W1_NS - 1) % W1_NS;
       wait_vm<(W1_NS - 3) * LPT>();  // tile i+1 has landed
-      __syncthreads();               // ... for every wavefront; all are done with tile i-1
+      // ... for every wavefront; all are done with tile i-1.  A bare barrier:
+      // __syncthreads()' fence would wait for every outstanding copy.
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wavefront's LDS reads are done
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __builtin_amdgcn_s_barrier();
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
       dma(cur, i + W1_NS - 1, stp);  // into tile i-1's stage
       bf16x8 kf[NQF], va[NDB][2];
       kfrags(st1, kf);  // every fragment read of the tile is in flight
@@ -949,6 +964,7 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
         __builtin_amdgcn_sched_group_barrier(0x002, QH == 1 ? 6 : 5, 0);  // VALU
       }
       __builtin_amdgcn_sched_barrier(0);
+      vties(va);
       if constexpr (QH == 2) {
         // ---- region 2
         pv(0, va, pf[0]);
