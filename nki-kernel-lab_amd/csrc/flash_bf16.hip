@@ -370,8 +370,15 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
           floatx16 sacc;
 #pragma unroll
           for (int e = 0; e < 16; ++e) sacc[e] = 0.f;
+          // Every K fragment read is in flight before the first MFMA waits
+          // for one (left to itself the compiler reads one fragment, waits for
+          // it and runs its MFMA, eight times over).
+          bf16x8 kf[NQF];
 #pragma unroll
-          for (int f = 0; f < NQF; ++f) sacc = MF::mma(load_frag(sb + kfrag_off + 16 * f), qf[f], sacc);
+          for (int f = 0; f < NQF; ++f) kf[f] = load_frag(sb + kfrag_off + 16 * f);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int f = 0; f < NQF; ++f) sacc = MF::mma(kf[f], qf[f], sacc);
           __builtin_amdgcn_sched_barrier(0);
           bf16x8 pf[2];
           softmax(k0, sacc, pf);
