@@ -96,6 +96,8 @@ struct Work {
   int grid;         // workgroups
   long units_head;  // units per head
   long units;       // total units
+  int cpb;          // balanced: cost charged at the start of every block, in units
+  long cost;        // balanced: total cost, units + cpb per block
   float* part;      // balanced: partial states [grid][2][PART]
   int part_bytes;   // balanced: bytes of part
   int* count;       // balanced: arrival counters [H][nqb], zero between calls
@@ -125,11 +127,48 @@ __device__ __forceinline__ long pair_before(int k, const Work& w) {
   return k == 0 ? 0 : k * full - delta;
 }
 
-__device__ __forceinline__ long range_start(long v, const Work& w) { return v * w.units / w.grid; }
+// Balanced ranges split a cost line evenly: the units in pair order, with
+// cpb units of cost in front of every block (a segment's fixed work: the
+// hand-over between the teams, the output or partial-state stores, the next
+// segment's first loads), so a workgroup whose range starts more blocks gets
+// fewer units.  Per head, pair k (blocks k and n-1-k) spans cost
+// [k F - delta, (k + 1) F - delta) with F = tpb (n + 1) + 2 cpb (pair 0 from 0):
+// cpb, block k's units, cpb, block n-1-k's units.  A range of more than cpb
+// cost holds at least one unit, which the planner guarantees.
+__device__ __forceinline__ long head_cost(const Work& w) { return w.units_head + (long)w.nqb * w.cpb; }
 
-// The workgroup (in range order) whose balanced range holds unit u.
+// Units (in pair order) whose cost position is below c.
+__device__ __forceinline__ long units_below_cost(long c, const Work& w) {
+  const long hc = head_cost(w);
+  const long hh = c / hc;
+  const long r = c - hh * hc;
+  const long F = (long)w.tpb * (w.nqb + 1) + 2L * w.cpb;
+  const long delta = (long)w.tpb * w.nqb - w.last_nt;
+  const int k = (int)min((r + delta) / F, (long)((w.nqb - 1) / 2));
+  const long o = r - (k == 0 ? 0 : k * F - delta);
+  const long na = block_tiles(k, w);
+  const long in_pair = o < w.cpb + na ? max(0L, o - w.cpb) : na + max(0L, o - 2L * w.cpb - na);
+  return hh * w.units_head + pair_before(k, w) + in_pair;
+}
+
+// Cost position of unit u.
+__device__ __forceinline__ long cost_of_unit(long u, const Work& w) {
+  const long hh = u / w.units_head;
+  const long r = u - hh * w.units_head;
+  const long full = (long)w.tpb * (w.nqb + 1);
+  const long delta = (long)w.tpb * w.nqb - w.last_nt;
+  const int k = (int)min((r + delta) / full, (long)((w.nqb - 1) / 2));
+  const long starts = r - pair_before(k, w) < block_tiles(k, w) ? 2 * k + 1 : 2 * k + 2;
+  return hh * head_cost(w) + r + starts * w.cpb;
+}
+
+// First unit of balanced range v (v = grid: the end of the last range).
+__device__ __forceinline__ long range_start(long v, const Work& w) { return units_below_cost(v * w.cost / w.grid, w); }
+
+// The balanced range that holds unit u: the one whose cost interval
+// [v cost / grid, (v + 1) cost / grid) holds u's cost position.
 __device__ __forceinline__ int range_of(long u, const Work& w) {
-  return (int)(((u + 1) * w.grid - 1) / w.units);
+  return (int)(((cost_of_unit(u, w) + 1) * w.grid - 1) / w.cost);
 }
 
 }  // namespace
@@ -201,6 +240,11 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
     int hh, b, t0, t1, nt;
     long bstart;
   };
+  // The segment of the range that ends with unit u.  A range is walked from
+  // its last segment to its first: the first segment in unit order is often
+  // the tail of a block whose head other workgroups hold, and taking it last
+  // leaves the merge of that block's partial states to this workgroup, the
+  // last to arrive, after its other segments rather than before them.
   auto decode = [&](long u) __attribute__((always_inline)) {
     Seg sg;
     sg.hh = (int)(u / w.units_head);
@@ -228,8 +272,8 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
     }
     sg.bstart = (long)sg.hh * w.units_head + before;
     sg.nt = block_tiles(sg.b, w);
-    sg.t0 = (int)(u - sg.bstart);
-    sg.t1 = (int)(min(u1, sg.bstart + sg.nt) - sg.bstart);
+    sg.t0 = (int)(max(u0, sg.bstart) - sg.bstart);
+    sg.t1 = (int)(u - sg.bstart + 1);
     return sg;
   };
   auto load_q = [&](const Seg& sg, bf16x8 (&q)[NQF]) __attribute__((always_inline)) {
@@ -273,7 +317,7 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
     }
   };
 
-  Seg cur = decode(u0);
+  Seg cur = decode(u1 - 1);
   bf16x8 qf[NQF];
   uint4 rk[CH], rv[CH];  // the next tile's K and V on their way to LDS
   load_q(cur, qf);
@@ -397,8 +441,8 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
     // their latency overlaps the hand-over between the teams and the stores
     // of this segment (issued after the stores they would wait for them too:
     // loads and stores share the vector memory counter).
-    const long next_u = bstart + t1;
-    const bool more = next_u < u1;
+    const long next_u = bstart + t0 - 1;  // the last unit of the previous segment
+    const bool more = next_u >= u0;
     Seg nxt = cur;
     if (more) nxt = decode(next_u);
     if (more) {
@@ -706,6 +750,11 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
     int hh, b, t0, t1, nt;
     long bstart;
   };
+  // The segment of the range that ends with unit u.  A range is walked from
+  // its last segment to its first: the first segment in unit order is often
+  // the tail of a block whose head other workgroups hold, and taking it last
+  // leaves the merge of that block's partial states to this workgroup, the
+  // last to arrive, after its other segments rather than before them.
   auto decode = [&](long u) __attribute__((always_inline)) {
     Seg sg;
     sg.hh = (int)(u / w.units_head);
@@ -733,8 +782,8 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
     }
     sg.bstart = (long)sg.hh * w.units_head + before;
     sg.nt = block_tiles(sg.b, w);
-    sg.t0 = (int)(u - sg.bstart);
-    sg.t1 = (int)(min(u1, sg.bstart + sg.nt) - sg.bstart);
+    sg.t0 = (int)(max(u0, sg.bstart) - sg.bstart);
+    sg.t1 = (int)(u - sg.bstart + 1);
     return sg;
   };
   bf16x8 qf[QH][NQF];
@@ -777,7 +826,7 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
     }
   };
 
-  Seg cur = decode(u0);
+  Seg cur = decode(u1 - 1);
   load_q(cur);
 
   for (;;) {
@@ -1064,8 +1113,8 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
       }
     };
 
-    const long next_u = bstart + t1;
-    const bool more = next_u < u1;
+    const long next_u = bstart + t0 - 1;  // the last unit of the previous segment
+    const bool more = next_u >= u0;
     Seg nxt = cur;
     if (more) nxt = decode(next_u);
 
@@ -1191,11 +1240,24 @@ Work plan(int H, int S, Config cfg) {
     const long by_size = (w.units + kMinUnits - 1) / kMinUnits;
     const int cus = cu_count() * wgs_per_cu(cfg.kern);
     w.grid = (int)(by_size < cus ? by_size : cus);
+    // Block start cost, in units: about a segment's fixed work over the time
+    // of one unit in the loop, tuned on MI355X (teams kernel, 8 x 2048: 31.2
+    // -> 27.4 us at 64-query blocks, 29.6 -> 27.1 at 128; 1 x 4096: 32.3 ->
+    // 24.8; 16 x 2048: 36.9 -> 34.1; the pipelined kernel's longer segments
+    // gain little).  At most a range's cost minus one, so that every range
+    // holds a unit.
+    const bool pipelined = cfg.kern == kW32x4 || cfg.kern == kW64x2 || cfg.kern == kW64x4 || cfg.kern == kW32x4x2;
+    int cpb = pipelined ? 2 : cfg.qb == 64 ? 10 : 5;
+    if (const char* f = getenv("NKL_FLASH_CPB")) cpb = atoi(f);
+    const long nblocks = (long)H * w.nqb;
+    while (cpb > 0 && (w.units + nblocks * cpb) / w.grid < cpb + 1) --cpb;
+    w.cpb = cpb < 0 ? 0 : cpb;
   } else if (cfg.sched == kPairs) {
     w.grid = H * ((w.nqb + 1) / 2);
   } else {
     w.grid = H * w.nqb;
   }
+  w.cost = w.units + (long)H * w.nqb * w.cpb;
   return w;
 }
 
