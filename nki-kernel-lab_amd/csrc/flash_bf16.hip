@@ -1241,13 +1241,14 @@ Work plan(int H, int S, Config cfg) {
     const int cus = cu_count() * wgs_per_cu(cfg.kern);
     w.grid = (int)(by_size < cus ? by_size : cus);
     // Block start cost, in units: about a segment's fixed work over the time
-    // of one unit in the loop, tuned on MI355X (teams kernel, 8 x 2048: 31.2
-    // -> 27.4 us at 64-query blocks, 29.6 -> 27.1 at 128; 1 x 4096: 32.3 ->
-    // 24.8; 16 x 2048: 36.9 -> 34.1; the pipelined kernel's longer segments
-    // gain little).  At most a range's cost minus one, so that every range
-    // holds a unit.
+    // of one unit in the loop, tuned on MI355X (teams kernel, 8 x 2048 at
+    // 128-query blocks: 29.6 -> 26.5 us; 1 x 4096 at 64: 32.3 -> 24.8;
+    // 16 x 2048: 36.9 -> 34.1; 8 x 4096: 53.1 -> 51.4; short ranges gain from
+    // a higher cost; the pipelined kernel's longer segments gain little).  At
+    // most a range's cost minus one, so that every range holds a unit.
     const bool pipelined = cfg.kern == kW32x4 || cfg.kern == kW64x2 || cfg.kern == kW64x4 || cfg.kern == kW32x4x2;
-    int cpb = pipelined ? 2 : cfg.qb == 64 ? 10 : 5;
+    const long per_wg = w.units / w.grid;
+    int cpb = pipelined ? 2 : cfg.qb == 64 ? 10 : per_wg < 20 ? 8 : 4;
     if (const char* f = getenv("NKL_FLASH_CPB")) cpb = atoi(f);
     const long nblocks = (long)H * w.nqb;
     while (cpb > 0 && (w.units + nblocks * cpb) / w.grid < cpb + 1) --cpb;
@@ -1262,8 +1263,8 @@ Work plan(int H, int S, Config cfg) {
 }
 
 // Schedule and kernel choice, from measured launches on MI355X (units of
-// 128-query blocks per CU): below 18, 64-query blocks halve the unit and keep
-// every CU busy (8 x 2048: 17); up to 200 the 8-wavefront teams kernel over
+// 128-query blocks per CU): below 12, 64-query blocks halve the unit and keep
+// every CU busy (1 x 4096: 8); up to 200 the 8-wavefront teams kernel over
 // balanced ranges (whole blocks leave CUs idle or unevenly loaded); from 200
 // the software-pipelined kernel at two wavefronts per SIMD (d > 64), whose
 // steady state is faster and whose longer segments amortise its start-up;
@@ -1276,7 +1277,7 @@ Config choose(int H, int S, int d) {
   const long cus = cu_count();
   const long nqb = (S + 127) / 128;
   const long units128 = (long)H * (2 * (nqb - 1) * nqb + (S - 1) / BN + 1);
-  Config cfg = units128 < 18 * cus     ? Config{64, kBalanced, kTeams}
+  Config cfg = units128 < 12 * cus     ? Config{64, kBalanced, kTeams}
                : units128 < 200 * cus  ? Config{128, kBalanced, kTeams}
                : units128 < 1024 * cus ? Config{128, kBalanced, kW32x4x2}
                                        : Config{128, kPairs, kW32x4x2};
