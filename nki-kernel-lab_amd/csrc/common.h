@@ -49,6 +49,20 @@ __device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w &
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// max / sum of x and x of lane l ^ 32, without the LDS: v_permlane32_swap
+// (gfx950) exchanges lanes 32-63 of its first operand with lanes 0-31 of its
+// second; with x in both, every lane ends up holding x of lanes l % 32 and
+// l % 32 + 32 in the two results.  (A ds_bpermute would also wait for every
+// LDS access of the wavefront still in flight.)
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // ------------------------------------------------------- 16-byte vectors --
 // VecE<T> = number of T elements in one 16-byte load.
 template <typename T>

@@ -354,7 +354,7 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
       float mloc = sc[0];
 #pragma unroll
       for (int e = 1; e < 16; ++e) mloc = fmaxf(mloc, sc[e]);
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave)) * c;
+      mloc = max_xor32(mloc) * c;
       if (__builtin_amdgcn_ballot_w64(mloc > m_run + kRescaleSlack)) {
         const float m_new = fmaxf(m_run, mloc);
         const float corr = fast_exp2(m_run - m_new);
@@ -463,7 +463,7 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
     // 4 db .. 4 db + 3 hold d-block db, chunk NCO holds (m, l).
     const int own0 = team * OWN;
     const bool keeps = own0 < NDB;
-    float l_tot = l_run + __shfl_xor(l_run, 32, kWave);  // lanes l and l ^ 32 hold the same query
+    float l_tot = sum_xor32(l_run);  // lanes l and l ^ 32 hold the same query
     if constexpr (NT > 1) {
       float4* xs = reinterpret_cast<float4*>(smem) + (team * WPT + wq) * (L::SLOT / 4) + lane;
 #pragma unroll
@@ -893,7 +893,7 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
       bool up = false;
 #pragma unroll
       for (int hq = 0; hq < QH; ++hq) {
-        mx[hq] = fmaxf(mx[hq], __shfl_xor(mx[hq], 32, kWave)) * c;
+        mx[hq] = max_xor32(mx[hq]) * c;
         up = up || mx[hq] > m_run[hq] + kRescaleSlack;
       }
       if (__builtin_amdgcn_ballot_w64(up)) {
@@ -1087,7 +1087,7 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
 
     float l_tot[QH];
 #pragma unroll
-    for (int hq = 0; hq < QH; ++hq) l_tot[hq] = l_run[hq] + __shfl_xor(l_run[hq], 32, kWave);
+    for (int hq = 0; hq < QH; ++hq) l_tot[hq] = sum_xor32(l_run[hq]);
     auto weights = [&](int hq, float m2, float l2, float& a1, float& a2) __attribute__((always_inline)) {
       const float M = fmaxf(m_run[hq], m2);
       a1 = m_run[hq] == -INFINITY ? 0.f : fast_exp2(m_run[hq] - M);
