@@ -181,6 +181,29 @@ def test_flash_bf16_schedules_agree_on_config(monkeypatch, qb, schedule):
     assert rel_err(out, _sdpa_cpu(*(_np(t) for t in (q, k, v)))) <= 3e-3
 
 
+@pytest.mark.parametrize("kernel,qb", [("teams", "64"), ("teams", "128"), ("teams4", "64"), ("w1o2", "128")])
+@pytest.mark.parametrize("cpb", ["0", "3", "15", "1000"])
+@pytest.mark.parametrize("H,S,d", [(8, 2048, 128), (3, 1537, 128), (5, 300, 64), (16, 640, 96)])
+def test_flash_bf16_balanced_block_start_cost(rng, monkeypatch, kernel, qb, cpb, H, S, d):
+    """The balanced split with block start costs from none to more than a
+    range holds (the planner lowers it until every range keeps a unit): every
+    unit is computed once and every split block merged once, whatever the
+    ranges; two calls in a row agree within the merge-order rounding."""
+    from nkilab import ops
+
+    monkeypatch.setenv("NKL_FLASH_KERNEL", kernel)
+    monkeypatch.setenv("NKL_FLASH_SCHEDULE", "balanced")
+    monkeypatch.setenv("NKL_FLASH_QB", qb)
+    monkeypatch.setenv("NKL_FLASH_CPB", cpb)
+    q, k, v = (_bf(rng.standard_normal((H, S, d))) for _ in range(3))
+    out = _np(ops.attention(q, k, v))
+    ref = _sdpa_cpu(*(_np(t) for t in (q, k, v)))
+    assert rel_err(out, ref) < 1e-2, (kernel, qb, cpb, H, S, d)
+    np.testing.assert_allclose(out[:, 0], _np(v)[:, 0], atol=1e-2)
+    again = _np(ops.attention(q, k, v))
+    assert np.abs(again - out).max() <= 2 ** -6 * max(1.0, float(np.abs(out).max()))
+
+
 # ------------------------------------------------ benchmark configurations --
 
 def test_causal_attention_8x2048x128_bf16_config():
