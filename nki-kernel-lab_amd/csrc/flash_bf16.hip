@@ -1246,16 +1246,19 @@ Work plan(int H, int S, Config cfg) {
     const int cus = cu_count() * wgs_per_cu(cfg.kern);
     w.grid = (int)(by_size < cus ? by_size : cus);
     // Block start cost, in units: about a segment's fixed work over the time
-    // of one unit in the loop, tuned on MI355X (teams kernel, 8 x 2048 at
-    // 128-query blocks: 29.6 -> 26.5 us; 1 x 4096 at 64: 32.3 -> 24.8;
-    // 16 x 2048: 36.9 -> 34.1; 8 x 4096: 53.1 -> 51.4; short ranges gain from
-    // a higher cost; the pipelined kernel's longer segments gain little).  At
-    // most a range's cost minus one, so that every range holds a unit.
+    // of one unit in the loop, tuned on MI355X with rotating inputs.  With
+    // fewer blocks than workgroups every block is split and a higher cost
+    // pays (teams kernel, 128-query blocks: 8 x 2048 28.9 -> 27.0 us at 12
+    // against 4; 12 x 2048 40.1 -> 34.4; 2 x 8192 57.3 -> 53.7); with at least
+    // as many, 4 is best (16 x 2048, 8 x 4096, 4 x 8192).  64-query blocks:
+    // 14 and 10 (1 x 4096: 32.3 -> 24.6 us against no cost); the pipelined
+    // kernel's longer segments gain little.  At most a range's cost minus
+    // one, so that every range holds a unit.
     const bool pipelined = cfg.kern == kW32x4 || cfg.kern == kW64x2 || cfg.kern == kW64x4 || cfg.kern == kW32x4x2;
-    const long per_wg = w.units / w.grid;
-    int cpb = pipelined ? 2 : cfg.qb == 64 ? 10 : per_wg < 20 ? 8 : 4;
-    if (const char* f = getenv("NKL_FLASH_CPB")) cpb = atoi(f);
     const long nblocks = (long)H * w.nqb;
+    const bool few = nblocks < w.grid;
+    int cpb = pipelined ? 2 : cfg.qb == 64 ? (few ? 14 : 10) : (few ? 12 : 4);
+    if (const char* f = getenv("NKL_FLASH_CPB")) cpb = atoi(f);
     while (cpb > 0 && (w.units + nblocks * cpb) / w.grid < cpb + 1) --cpb;
     w.cpb = cpb < 0 ? 0 : cpb;
   } else if (cfg.sched == kPairs) {
