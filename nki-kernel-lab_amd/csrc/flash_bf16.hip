@@ -1259,7 +1259,7 @@ Work plan(int H, int S, Config cfg) {
     const long nblocks = (long)H * w.nqb;
     const bool few = nblocks < w.grid;
     int cpb = pipelined ? 2 : cfg.qb == 64 ? (few ? 14 : 10) : (few ? 12 : 4);
-    if (const char* f = getenv("NKL_FLASH_CPB")) cpb = atoi(f);
+    if (const char* f = getenv("NKL_FLASH_CPB")) cpb = min(max(atoi(f), 0), 4096);
     while (cpb > 0 && (w.units + nblocks * cpb) / w.grid < cpb + 1) --cpb;
     w.cpb = cpb < 0 ? 0 : cpb;
   } else if (cfg.sched == kPairs) {
