@@ -1,7 +1,8 @@
 """NumPy restatement of the reference's NKI kernel set -- the ORACLE.
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
-bench.py's CPU-baseline leg as the checker; never by the nkilab product.
+bench.py's CPU-baseline leg, as the reference that results are compared
+against; never by the nkilab product.
 
 Conventions.  Arrays are np.float32.  A bfloat16 tensor is an np.float32 array
 whose values are all bf16-representable, tagged by a ``dtype`` argument
