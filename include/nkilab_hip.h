@@ -189,6 +189,25 @@ int nkl_flash_attn_causal_ws(const void* q, const void* k, const void* v,
                              float scale, int dtype, void* stream);
 
 /*
+ * Process-wide choice of the bf16 causal-attention kernel and schedule, for
+ * tests and tuning (no counterpart in the reference).  Each argument is -1
+ * for the automatic choice, or:
+ *   kernel:   0 teams, 1 one wavefront per SIMD (32 queries), 2 (64 queries,
+ *             2 wavefronts), 3 (64 queries, 4 wavefronts), 4 4-wavefront
+ *             teams, 5 one-wavefront kernel at two per SIMD, 6 the
+ *             64-key-tile kernel (d > 64 only);
+ *   schedule: 0 block, 1 balanced (needs the scratch of
+ *             nkl_flash_attn_causal_ws), 2 pairs;
+ *   qb:       64 or 128 queries per block (kernels 0 and 4);
+ *   cpb:      balanced schedule, cost charged per block start, 0..4096.
+ * Without a call the choice is read once from NKL_FLASH_KERNEL,
+ * NKL_FLASH_SCHEDULE, NKL_FLASH_QB and NKL_FLASH_CPB.  The workspace sizes
+ * follow the configuration in force when they are queried; do not change it
+ * while another thread sizes or launches attention.
+ */
+int nkl_flash_attn_configure(int kernel, int schedule, int qb, int cpb);
+
+/*
  * Unfused causal attention: scores (fp32, [H, S, S]) and probabilities
  * ([H, S, S], dtype) are materialised in `workspace`, then O = P V.
  * Replaces nkilab/kernels/attention.py:35 (attention_naive), selected by

@@ -407,6 +407,10 @@ extern "C" int nkl_flash_attn_causal_gqa(const void* q, const void* k, const voi
                      true, H, Hkv, S, d, strides, scale, dtype, stream);
 }
 
+extern "C" int nkl_flash_attn_configure(int kernel, int schedule, int qb, int cpb) {
+  return flash_bf16_configure(kernel, schedule, qb, cpb);
+}
+
 extern "C" size_t nkl_attention_naive_workspace_bytes(int H, int S, int dtype) {
   if (H <= 0 || S <= 0) return 0;
   const size_t n = (size_t)H * S * S;

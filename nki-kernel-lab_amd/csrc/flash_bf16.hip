@@ -42,31 +42,18 @@
 #include <string.h>
 
 #include "attention.h"
+#include "flash_sched.h"
 
 namespace nkl {
 
 namespace {
 
+using namespace fsched;
+
 constexpr int BN = 32;  // keys per tile
-// Buffer-resource word 3 for raw (untyped) dword loads on gfx9-family GPUs.
-constexpr int kBufferFlags = 0x00020000;
-// The running max is only raised (and O, l rescaled) when a score exceeds it
-// by more than 2^8 in the exp2 domain: until then p = exp2(s c - m) stays
-// below 256, which fp32 sums and bf16 probabilities represent with the same
-// relative precision, and the final O / l is unchanged.
-constexpr float kRescaleSlack = 8.0f;
 // Smallest unit range a workgroup is given in the balanced schedule (16 left
 // half the CUs idle at 2 x 2048: 24.7 -> 20.6 us at 8; 2 x 1024: 25.5 -> 17.6).
 constexpr long kMinUnits = 8;
-// Cache policy of the partial-state stores and loads: SC1, coherent at device
-// scope (the same policy as an agent-scope atomic load or store).  Partial
-// states travel between workgroups on different XCDs; with every store and
-// load of them device-coherent, the hand-off needs no L2 writeback or
-// invalidate -- only each store's completion (vmcnt) before the arrival
-// atomic.
-constexpr int kDeviceCoherent = 16;
-
-enum Sched { kBlock = 0, kBalanced = 1, kPairs = 2 };
 
 template <int D, int WPT, int NT>
 struct Layout {
@@ -88,21 +75,6 @@ struct Layout {
   static constexpr int SMEM = NT == 1 || TOTAL * 2 > XBYTES ? TOTAL : XBYTES / 2;
 };
 
-struct Work {
-  int nqb;          // query blocks per head
-  int tpb;          // key tiles added per block (QB / BN): block b has tpb (b + 1)
-  int last_nt;      // key tiles of the last (possibly partial) block
-  int paired;       // unit order: 1 pair order, 0 block order
-  int sched;        // Sched
-  int grid;         // workgroups
-  long units_head;  // units per head
-  long units;       // total units
-  int cpb;          // balanced: cost charged at the start of every block, in units
-  long cost;        // balanced: total cost, units + cpb per block
-  float* part;      // balanced: partial states [grid][2][PART]
-  int part_bytes;   // balanced: bytes of part
-  int* count;       // balanced: arrival counters [H][nqb], zero between calls
-};
 
 __device__ __forceinline__ bf16x8 read_vt_frag(const bf16* row_a, const bf16* row_b) {
   typedef short shortx4 __attribute__((ext_vector_type(4)));
@@ -114,63 +86,6 @@ __device__ __forceinline__ bf16x8 read_vt_frag(const bf16* row_a, const bf16* ro
   return __builtin_bit_cast(bf16x8, c);
 }
 
-__device__ __forceinline__ int block_tiles(int b, const Work& w) {
-  return b == w.nqb - 1 ? w.last_nt : w.tpb * (b + 1);
-}
-// Block order: units of a head before block b.
-__device__ __forceinline__ long plain_before(int b, const Work& w) { return (long)w.tpb * b * (b + 1) / 2; }
-// Pair order: units of a head before pair k (blocks k and n-1-k).  Every pair
-// but the first holds tpb (n + 1) units; the first lacks the last block's
-// missing tiles (tpb n - last_nt).
-__device__ __forceinline__ long pair_before(int k, const Work& w) {
-  const long full = (long)w.tpb * (w.nqb + 1);
-  const long delta = (long)w.tpb * w.nqb - w.last_nt;
-  return k == 0 ? 0 : k * full - delta;
-}
-
-// Balanced ranges split a cost line evenly: the units in pair order, with
-// cpb units of cost in front of every block (a segment's fixed work: the
-// hand-over between the teams, the output or partial-state stores, the next
-// segment's first loads), so a workgroup whose range starts more blocks gets
-// fewer units.  Per head, pair k (blocks k and n-1-k) spans cost
-// [k F - delta, (k + 1) F - delta) with F = tpb (n + 1) + 2 cpb (pair 0 from 0):
-// cpb, block k's units, cpb, block n-1-k's units.  A range of more than cpb
-// cost holds at least one unit, which the planner guarantees.
-__device__ __forceinline__ long head_cost(const Work& w) { return w.units_head + (long)w.nqb * w.cpb; }
-
-// Units (in pair order) whose cost position is below c.
-__device__ __forceinline__ long units_below_cost(long c, const Work& w) {
-  const long hc = head_cost(w);
-  const long hh = c / hc;
-  const long r = c - hh * hc;
-  const long F = (long)w.tpb * (w.nqb + 1) + 2L * w.cpb;
-  const long delta = (long)w.tpb * w.nqb - w.last_nt;
-  const int k = (int)min((r + delta) / F, (long)((w.nqb - 1) / 2));
-  const long o = r - (k == 0 ? 0 : k * F - delta);
-  const long na = block_tiles(k, w);
-  const long in_pair = o < w.cpb + na ? max(0L, o - w.cpb) : na + max(0L, o - 2L * w.cpb - na);
-  return hh * w.units_head + pair_before(k, w) + in_pair;
-}
-
-// Cost position of unit u.
-__device__ __forceinline__ long cost_of_unit(long u, const Work& w) {
-  const long hh = u / w.units_head;
-  const long r = u - hh * w.units_head;
-  const long full = (long)w.tpb * (w.nqb + 1);
-  const long delta = (long)w.tpb * w.nqb - w.last_nt;
-  const int k = (int)min((r + delta) / full, (long)((w.nqb - 1) / 2));
-  const long starts = r - pair_before(k, w) < block_tiles(k, w) ? 2 * k + 1 : 2 * k + 2;
-  return hh * head_cost(w) + r + starts * w.cpb;
-}
-
-// First unit of balanced range v (v = grid: the end of the last range).
-__device__ __forceinline__ long range_start(long v, const Work& w) { return units_below_cost(v * w.cost / w.grid, w); }
-
-// The balanced range that holds unit u: the one whose cost interval
-// [v cost / grid, (v + 1) cost / grid) holds u's cost position.
-__device__ __forceinline__ int range_of(long u, const Work& w) {
-  return (int)(((cost_of_unit(u, w) + 1) * w.grid - 1) / w.cost);
-}
 
 }  // namespace
 
@@ -646,8 +561,8 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
 // global -> LDS by the buffer unit (buffer_load ... lds: lane l's 16 bytes
 // land at the instruction's LDS base + 16 l), W1_NS - 2 tiles ahead of use,
 // into W1_NS stages of unpadded 256-byte rows whose 16-byte chunks are
-// swizzled: logical chunk c of row r sits at chunk c ^ w1_swz(r), with
-// w1_swz(r) = 4 (r % 4) + 2 ((r / 4) % 2) + (r / 8) % 2.  The 16 rows of a
+// swizzled: logical chunk c of row r sits at chunk c ^ row_swz(r), with
+// row_swz(r) = 4 (r % 4) + 2 ((r / 4) % 2) + (r / 8) % 2.  The 16 rows of a
 // K-fragment read (b128, one chunk each, also as rows 0-7 x chunks 2f, 2f+1)
 // and the 4 aligned rows x 4 aligned chunks of a transposed V read (b64)
 // then all fall in distinct bank groups.  W1_NS = 4 stages of 16 KB keep
@@ -660,15 +575,6 @@ constexpr int W1_NS = 4;                    // LDS stages (offsets stay below 64
 constexpr int W1_ROWB = 256;                // bytes of a K/V row (d = 128)
 constexpr int W1_TILEB = BN * W1_ROWB;      // bytes of a K (or V) tile
 constexpr int W1_STAGEB = 2 * W1_TILEB;     // K tile then V tile
-
-__device__ __forceinline__ int w1_swz(int r) { return ((r & 3) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1); }
-
-// s_waitcnt with vmcnt <= n and the other counters left alone (gfx9 encoding).
-template <int n>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(n >= 0 && n < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 
 }  // namespace
 
@@ -700,7 +606,7 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
   //   K fragment f: row l32, logical chunk 2 f + h32.
   int koff[NQF];
   {
-    const int sw = w1_swz(l32);
+    const int sw = row_swz(l32);
 #pragma unroll
     for (int f = 0; f < NQF; ++f) koff[f] = l32 * W1_ROWB + (((2 * f + h32) ^ sw) << 4);
   }
@@ -716,7 +622,7 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         const int row = r0 + 8 * half;
-        voff[db][half] = W1_TILEB + row * W1_ROWB + (((4 * db + cb) ^ w1_swz(row)) << 4) + (i16 & 1) * 8;
+        voff[db][half] = W1_TILEB + row * W1_ROWB + (((4 * db + cb) ^ row_swz(row)) << 4) + (i16 & 1) * 8;
       }
   }
   //   DMA: this wavefront copies rows 4 NI wq .. 4 NI (wq + 1) - 1 of each
@@ -728,7 +634,7 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
 #pragma unroll
   for (int u = 0; u < NI; ++u) {
     const int row = 4 * (NI * wq + u) + (lane >> 4);
-    const int lc = (lane & 15) ^ w1_swz(row);
+    const int lc = (lane & 15) ^ row_swz(row);
     const bool ok = lc * 8 < dlim;
     dk[u] = ok ? 2 * (row * (int)p.k_ss + lc * 8) : 0x40000000;
     dv[u] = ok ? 2 * (row * (int)p.v_ss + lc * 8) : 0x40000000;
@@ -1213,8 +1119,63 @@ int cu_count() {
 // 4 with two workgroups per CU); the software-pipelined kernel with one
 // wavefront per SIMD and 32 queries (4 per workgroup) or 64 queries (2 or 4
 // per workgroup); or that kernel with 32 queries at two wavefronts per SIMD
-// (256 registers each, two independent workgroups per CU).
-enum Kern { kTeams = 0, kW32x4 = 1, kW64x2 = 2, kW64x4 = 3, kTeams4 = 4, kW32x4x2 = 5 };
+// (256 registers each, two independent workgroups per CU); or the
+// 64-key-tile kernel of flash_fwd.hip (kFwd: 128-query blocks, two
+// wavefronts per SIMD splitting each tile's keys, LDS-DMA stages).
+enum Kern { kTeams = 0, kW32x4 = 1, kW64x2 = 2, kW64x4 = 3, kTeams4 = 4, kW32x4x2 = 5, kFwd = 6 };
+
+// Launch-configuration overrides (-1: the automatic choice), process-wide:
+// read from the environment once, at first use -- NKL_FLASH_SCHEDULE=
+// block|pairs|balanced, NKL_FLASH_QB=64|128,
+// NKL_FLASH_KERNEL=teams|teams4|w1|w1o2|w64|w64x4|fwd, NKL_FLASH_CPB=<units>
+// -- or set by nkl_flash_attn_configure() (tests, tuning), so that a
+// workspace sized by one call fits the launch of the next.
+struct Overrides {
+  int sched = -1, qb = -1, kern = -1, cpb = -1;
+};
+Overrides& overrides() {
+  static Overrides o = [] {
+    Overrides r;
+    if (const char* f = getenv("NKL_FLASH_SCHEDULE")) {
+      if (!strcmp(f, "block")) r.sched = kBlock;
+      if (!strcmp(f, "pairs")) r.sched = kPairs;
+      if (!strcmp(f, "balanced")) r.sched = kBalanced;
+    }
+    if (const char* f = getenv("NKL_FLASH_QB")) {
+      if (!strcmp(f, "64")) r.qb = 64;
+      if (!strcmp(f, "128")) r.qb = 128;
+    }
+    if (const char* f = getenv("NKL_FLASH_KERNEL")) {
+      if (!strcmp(f, "teams")) r.kern = kTeams;
+      if (!strcmp(f, "teams4")) r.kern = kTeams4;
+      if (!strcmp(f, "w1")) r.kern = kW32x4;
+      if (!strcmp(f, "w1o2")) r.kern = kW32x4x2;
+      if (!strcmp(f, "w64")) r.kern = kW64x2;
+      if (!strcmp(f, "w64x4")) r.kern = kW64x4;
+      if (!strcmp(f, "fwd")) r.kern = kFwd;
+    }
+    if (const char* f = getenv("NKL_FLASH_CPB")) r.cpb = min(max(atoi(f), 0), 4096);
+    return r;
+  }();
+  return o;
+}
+
+}  // namespace
+
+int flash_bf16_configure(int kern, int sched, int qb, int cpb) {
+  if (kern < -1 || kern > kFwd || sched < -1 || sched > kPairs || (qb != -1 && qb != 64 && qb != 128) || cpb < -1 ||
+      cpb > 4096)
+    return set_error(NKL_EINVAL, "nkl_flash_attn_configure: kernel %d, schedule %d, qb %d, cpb %d out of range", kern,
+                     sched, qb, cpb);
+  Overrides& o = overrides();
+  o.kern = kern;
+  o.sched = sched;
+  o.qb = qb;
+  o.cpb = cpb;
+  return NKL_OK;
+}
+
+namespace {
 
 // A launch configuration: queries per block, a schedule and a kernel.  The
 // teams kernel takes 64-query blocks (2 wavefronts x 4 teams, or x 2 teams in
@@ -1232,9 +1193,10 @@ int wgs_per_cu(int kern) { return kern == kW64x2 || kern == kTeams4 || kern == k
 
 Work plan(int H, int S, Config cfg) {
   Work w{};
-  w.tpb = cfg.qb / BN;
+  const int bn = cfg.kern == kFwd ? 64 : BN;  // keys per tile
+  w.tpb = cfg.qb / bn;
   w.nqb = (S + cfg.qb - 1) / cfg.qb;
-  w.last_nt = (S - 1) / BN + 1;
+  w.last_nt = (S - 1) / bn + 1;
   w.units_head = (long)w.tpb * (w.nqb - 1) * w.nqb / 2 + w.last_nt;
   w.units = (long)H * w.units_head;
   w.sched = cfg.sched;
@@ -1258,8 +1220,8 @@ Work plan(int H, int S, Config cfg) {
     const bool pipelined = cfg.kern == kW32x4 || cfg.kern == kW64x2 || cfg.kern == kW64x4 || cfg.kern == kW32x4x2;
     const long nblocks = (long)H * w.nqb;
     const bool few = nblocks < w.grid;
-    int cpb = pipelined ? 2 : cfg.qb == 64 ? (few ? 14 : 10) : (few ? 12 : 4);
-    if (const char* f = getenv("NKL_FLASH_CPB")) cpb = min(max(atoi(f), 0), 4096);
+    int cpb = cfg.kern == kFwd ? 4 : pipelined ? 2 : cfg.qb == 64 ? (few ? 14 : 10) : (few ? 12 : 4);
+    if (overrides().cpb >= 0) cpb = overrides().cpb;
     while (cpb > 0 && (w.units + nblocks * cpb) / w.grid < cpb + 1) --cpb;
     w.cpb = cpb < 0 ? 0 : cpb;
   } else if (cfg.sched == kPairs) {
@@ -1279,9 +1241,8 @@ Work plan(int H, int S, Config cfg) {
 // steady state is faster and whose longer segments amortise its start-up;
 // from 1024 one workgroup per pair of blocks, which balances as well and
 // needs no partial states.
-// NKL_FLASH_SCHEDULE=block|pairs|balanced, NKL_FLASH_QB=64|128 and
-// NKL_FLASH_KERNEL=teams|teams4|w1|w1o2|w64|w64x4 override the choice (tests, tuning);
-// the one-wavefront-per-SIMD kernels take 64 < d <= 128 and fix the block.
+// The overrides above replace the choice (tests, tuning); the
+// one-wavefront-per-SIMD kernels and kFwd take 64 < d <= 128 and fix the block.
 Config choose(int H, int S, int d) {
   const long cus = cu_count();
   const long nqb = (S + 127) / 128;
@@ -1290,25 +1251,12 @@ Config choose(int H, int S, int d) {
                : units128 < 200 * cus  ? Config{128, kBalanced, kTeams}
                : units128 < 1024 * cus ? Config{128, kBalanced, kW32x4x2}
                                        : Config{128, kPairs, kW32x4x2};
-  if (const char* f = getenv("NKL_FLASH_SCHEDULE")) {
-    if (!strcmp(f, "block")) cfg.sched = kBlock;
-    if (!strcmp(f, "pairs")) cfg.sched = kPairs;
-    if (!strcmp(f, "balanced")) cfg.sched = kBalanced;
-  }
-  if (const char* f = getenv("NKL_FLASH_QB")) {
-    if (!strcmp(f, "64")) cfg.qb = 64;
-    if (!strcmp(f, "128")) cfg.qb = 128;
-  }
-  if (const char* f = getenv("NKL_FLASH_KERNEL")) {
-    if (!strcmp(f, "teams")) cfg.kern = kTeams;
-    if (!strcmp(f, "teams4")) cfg.kern = kTeams4;
-    if (!strcmp(f, "w1")) cfg.kern = kW32x4;
-    if (!strcmp(f, "w1o2")) cfg.kern = kW32x4x2;
-    if (!strcmp(f, "w64")) cfg.kern = kW64x2;
-    if (!strcmp(f, "w64x4")) cfg.kern = kW64x4;
-  }
+  const Overrides& ov = overrides();
+  if (ov.sched >= 0) cfg.sched = ov.sched;
+  if (ov.qb >= 0) cfg.qb = ov.qb;
+  if (ov.kern >= 0) cfg.kern = ov.kern;
   if (d <= 64 && cfg.kern != kTeams4) cfg.kern = kTeams;
-  if (cfg.kern == kW32x4 || cfg.kern == kW64x2 || cfg.kern == kW32x4x2) cfg.qb = 128;
+  if (cfg.kern == kW32x4 || cfg.kern == kW64x2 || cfg.kern == kW32x4x2 || cfg.kern == kFwd) cfg.qb = 128;
   if (cfg.kern == kW64x4) cfg.qb = 256;
   return cfg;
 }
@@ -1321,8 +1269,9 @@ size_t part_floats(int qb) {
   return qb == 64 ? Layout<D, 2, 4>::PART : (size_t)(qb / 128) * Layout<D, 4, 2>::PART;
 }
 
-size_t part_floats_for(int d, int qb) {
-  return d <= 32 ? part_floats<32>(qb) : d <= 64 ? part_floats<64>(qb) : part_floats<128>(qb);
+size_t part_floats_for(int d, const Config& cfg) {
+  if (cfg.kern == kFwd) return flash_fwd_part_bytes() / 4;
+  return d <= 32 ? part_floats<32>(cfg.qb) : d <= 64 ? part_floats<64>(cfg.qb) : part_floats<128>(cfg.qb);
 }
 
 template <int D, int WPT, int NT>
@@ -1355,7 +1304,7 @@ size_t flash_bf16_workspace_bytes(int H, int S, int d) {
   if (H <= 0 || S <= 0) return 0;
   const Config cfg = choose(H, S, d);
   if (cfg.sched != kBalanced) return 0;
-  return (size_t)plan(H, S, cfg).grid * 2 * part_floats_for(d, cfg.qb) * 4;
+  return (size_t)plan(H, S, cfg).grid * 2 * part_floats_for(d, cfg) * 4;
 }
 
 // The counters do not depend on d: one per 64-query block (the smallest
@@ -1381,6 +1330,10 @@ int flash_bf16_launch(const AttnArgs& a, void* workspace, size_t workspace_bytes
     w.part = static_cast<float*>(workspace);
     w.part_bytes = (int)need;
     w.count = counters;
+  }
+  if (cfg.kern == kFwd) {
+    launch_flash_fwd(a, w, st);
+    return check_launch("nkl_flash_attn_causal");
   }
   if (cfg.kern == kW32x4 || cfg.kern == kW64x2 || cfg.kern == kW64x4 || cfg.kern == kW32x4x2) {
     if (cfg.kern == kW32x4)

@@ -47,6 +47,7 @@ SIGNATURES = {
                                          _c_int, _vp]),
     "nkl_rope": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _c_long, _c_long, _c_long, _c_long, _c_int, _c_float,
                           _c_int, _vp]),
+    "nkl_flash_attn_configure": (_c_int, [_c_int, _c_int, _c_int, _c_int]),
     "nkl_attention_naive_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int]),
     "nkl_attention_naive": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_size, _c_int, _c_int, _c_int, _c_long, _c_long,
                                      _c_long, _c_long, _c_long, _c_long, _c_long, _c_long, _c_float, _c_int, _vp]),
@@ -78,6 +79,19 @@ def lib() -> ctypes.CDLL:
             raise RuntimeError(f"{LIB_PATH} has ABI version {ver}, expected {ABI_VERSION}; rebuild it")
         _lib = handle
     return _lib
+
+
+# Codes of nkl_flash_attn_configure (include/nkilab_hip.h).
+FLASH_KERNELS = {"teams": 0, "w1": 1, "w64": 2, "w64x4": 3, "teams4": 4, "w1o2": 5, "fwd": 6}
+FLASH_SCHEDULES = {"block": 0, "balanced": 1, "pairs": 2}
+
+
+def flash_configure(kernel: str | None = None, schedule: str | None = None, qb: int | None = None,
+                    cpb: int | None = None) -> None:
+    """Force the bf16 attention kernel / schedule / block / block start cost
+    (None: the automatic choice) for every later call in this process."""
+    call("nkl_flash_attn_configure", FLASH_KERNELS[kernel] if kernel else -1,
+         FLASH_SCHEDULES[schedule] if schedule else -1, int(qb) if qb else -1, -1 if cpb is None else int(cpb))
 
 
 def call(name: str, *args) -> int:

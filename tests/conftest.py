@@ -47,3 +47,13 @@ def assert_within_bf16_ulps(out, ref, ulps=1.0, floor=0.0):
 
 def load_golden(name):
     return dict(np.load(os.path.join(GOLDEN_DIR, name + ".npz"), allow_pickle=False))
+
+
+@pytest.fixture
+def flash_cfg():
+    """Force the bf16 attention kernel / schedule / block / block start cost for
+    one test (nkl_flash_attn_configure), restoring the automatic choice after."""
+    from nkilab import _lib
+
+    yield _lib.flash_configure
+    _lib.flash_configure()

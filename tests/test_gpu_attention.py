@@ -121,16 +121,14 @@ SCHEDULES = [(qb, s) for qb in ("64", "128") for s in ("balanced", "pairs", "blo
 @pytest.mark.parametrize("qb,schedule", SCHEDULES)
 @pytest.mark.parametrize("H,S,d", [(1, 1, 64), (2, 65, 32), (3, 77, 128), (1, 300, 128), (4, 1000, 64),
                                    (2, 1537, 128), (5, 640, 96), (1, 129, 128), (1, 192, 128)])
-def test_flash_bf16_schedules(rng, monkeypatch, kernel, qb, schedule, H, S, d):
+def test_flash_bf16_schedules(rng, flash_cfg, kernel, qb, schedule, H, S, d):
     """Every configuration of the bf16 teams kernel -- 8 or 4 wavefronts; 64-
     or 128-query blocks; split blocks merged by the last workgroup, one
     workgroup per pair of blocks, or one per block -- on ragged S and several
     head dims."""
     from nkilab import ops
 
-    monkeypatch.setenv("NKL_FLASH_KERNEL", kernel)
-    monkeypatch.setenv("NKL_FLASH_SCHEDULE", schedule)
-    monkeypatch.setenv("NKL_FLASH_QB", qb)
+    flash_cfg(kernel=kernel, schedule=schedule, qb=qb)
     q, k, v = (_bf(rng.standard_normal((H, S, d))) for _ in range(3))
     out = _np(ops.attention(q, k, v))
     ref = _sdpa_cpu(*(_np(t) for t in (q, k, v)))
@@ -138,17 +136,16 @@ def test_flash_bf16_schedules(rng, monkeypatch, kernel, qb, schedule, H, S, d):
     np.testing.assert_allclose(out[:, 0], _np(v)[:, 0], atol=1e-2)  # query 0 sees only key 0
 
 
-@pytest.mark.parametrize("kernel", ["w1", "w1o2", "w64", "w64x4"])
+@pytest.mark.parametrize("kernel", ["w1", "w1o2", "w64", "w64x4", "fwd"])
 @pytest.mark.parametrize("schedule", ["balanced", "pairs", "block"])
 @pytest.mark.parametrize("H,S,d", [(1, 1, 128), (3, 77, 128), (1, 300, 128), (2, 1537, 128), (5, 640, 96),
                                    (1, 129, 128), (2, 4096, 128), (4, 257, 72)])
-def test_flash_bf16_one_wave_per_simd_kernel(rng, monkeypatch, kernel, schedule, H, S, d):
+def test_flash_bf16_one_wave_per_simd_kernel(rng, flash_cfg, kernel, schedule, H, S, d):
     """The one-wavefront-per-SIMD kernels (LDS-DMA staging, swizzled rows) under
     each schedule: 32 queries x 4 wavefronts, 64 x 2 and 64 x 4."""
     from nkilab import ops
 
-    monkeypatch.setenv("NKL_FLASH_KERNEL", kernel)
-    monkeypatch.setenv("NKL_FLASH_SCHEDULE", schedule)
+    flash_cfg(kernel=kernel, schedule=schedule)
     q, k, v = (_bf(rng.standard_normal((H, S, d))) for _ in range(3))
     out = _np(ops.attention(q, k, v))
     ref = _sdpa_cpu(*(_np(t) for t in (q, k, v)))
@@ -156,45 +153,41 @@ def test_flash_bf16_one_wave_per_simd_kernel(rng, monkeypatch, kernel, schedule,
     np.testing.assert_allclose(out[:, 0], _np(v)[:, 0], atol=1e-2)
 
 
-@pytest.mark.parametrize("kernel", ["w1", "w1o2", "w64", "w64x4", "teams4"])
-def test_flash_bf16_one_wave_per_simd_config(monkeypatch, kernel):
+@pytest.mark.parametrize("kernel", ["w1", "w1o2", "w64", "w64x4", "teams4", "fwd"])
+def test_flash_bf16_one_wave_per_simd_config(flash_cfg, kernel):
     """8 x 2048 x 128 through each one-wavefront-per-SIMD kernel (balanced):
     within 3e-3 of fp32 SDPA."""
     from nkilab import ops, workloads
 
-    monkeypatch.setenv("NKL_FLASH_KERNEL", kernel)
-    monkeypatch.setenv("NKL_FLASH_SCHEDULE", "balanced")
+    flash_cfg(kernel=kernel, schedule="balanced")
     q, k, v = (t.cuda() for t in workloads.attention_inputs())
     out = _np(ops.attention(q, k, v))
     assert rel_err(out, _sdpa_cpu(*(_np(t) for t in (q, k, v)))) <= 3e-3
 
 
 @pytest.mark.parametrize("qb,schedule", SCHEDULES)
-def test_flash_bf16_schedules_agree_on_config(monkeypatch, qb, schedule):
+def test_flash_bf16_schedules_agree_on_config(flash_cfg, qb, schedule):
     """8 x 2048 x 128 under each configuration: within 3e-3 of fp32 SDPA."""
     from nkilab import ops, workloads
 
-    monkeypatch.setenv("NKL_FLASH_SCHEDULE", schedule)
-    monkeypatch.setenv("NKL_FLASH_QB", qb)
+    flash_cfg(schedule=schedule, qb=qb)
     q, k, v = (t.cuda() for t in workloads.attention_inputs())
     out = _np(ops.attention(q, k, v))
     assert rel_err(out, _sdpa_cpu(*(_np(t) for t in (q, k, v)))) <= 3e-3
 
 
-@pytest.mark.parametrize("kernel,qb", [("teams", "64"), ("teams", "128"), ("teams4", "64"), ("w1o2", "128")])
+@pytest.mark.parametrize("kernel,qb", [("teams", "64"), ("teams", "128"), ("teams4", "64"), ("w1o2", "128"),
+                                       ("fwd", "128")])
 @pytest.mark.parametrize("cpb", ["0", "3", "15", "1000"])
 @pytest.mark.parametrize("H,S,d", [(8, 2048, 128), (3, 1537, 128), (5, 300, 64), (16, 640, 96)])
-def test_flash_bf16_balanced_block_start_cost(rng, monkeypatch, kernel, qb, cpb, H, S, d):
+def test_flash_bf16_balanced_block_start_cost(rng, flash_cfg, kernel, qb, cpb, H, S, d):
     """The balanced split with block start costs from none to more than a
     range holds (the planner lowers it until every range keeps a unit): every
     unit is computed once and every split block merged once, whatever the
     ranges; two calls in a row agree within the merge-order rounding."""
     from nkilab import ops
 
-    monkeypatch.setenv("NKL_FLASH_KERNEL", kernel)
-    monkeypatch.setenv("NKL_FLASH_SCHEDULE", "balanced")
-    monkeypatch.setenv("NKL_FLASH_QB", qb)
-    monkeypatch.setenv("NKL_FLASH_CPB", cpb)
+    flash_cfg(kernel=kernel, schedule="balanced", qb=qb, cpb=cpb)
     q, k, v = (_bf(rng.standard_normal((H, S, d))) for _ in range(3))
     out = _np(ops.attention(q, k, v))
     ref = _sdpa_cpu(*(_np(t) for t in (q, k, v)))
@@ -290,13 +283,12 @@ def test_gqa_attention_matches_sdpa_on_repeated_kv(rng, variant, H, Hkv, S, d):
 
 @pytest.mark.parametrize("kernel,qb,schedule", [("teams", "128", "balanced"), ("teams", "64", "balanced"),
                                                 ("teams", "128", "pairs"), ("teams", "128", "block"),
-                                                ("w64", "128", "balanced"), ("teams4", "64", "balanced")])
-def test_gqa_bf16_every_kernel_and_schedule(rng, monkeypatch, kernel, qb, schedule):
+                                                ("w64", "128", "balanced"), ("teams4", "64", "balanced"),
+                                                ("fwd", "128", "balanced"), ("fwd", "128", "pairs")])
+def test_gqa_bf16_every_kernel_and_schedule(rng, flash_cfg, kernel, qb, schedule):
     from nkilab import ops
 
-    monkeypatch.setenv("NKL_FLASH_KERNEL", kernel)
-    monkeypatch.setenv("NKL_FLASH_SCHEDULE", schedule)
-    monkeypatch.setenv("NKL_FLASH_QB", qb)
+    flash_cfg(kernel=kernel, schedule=schedule, qb=qb)
     H, Hkv, S, d = 8, 2, 1537, 128
     q = _bf(rng.standard_normal((H, S, d)))
     k, v = (_bf(rng.standard_normal((Hkv, S, d))) for _ in range(2))
