@@ -130,11 +130,35 @@ int nkl_rmsnorm(const void* x, const void* w, void* y, int rows, int cols,
                 void* stream);
 
 /*
+ * The same RMSNorm with the weight in its own dtype (dtype_w in {F32, BF16},
+ * independent of dtype_in): the fp32 normalised row is multiplied by the
+ * weight as stored, then rounded once, as nkilab/kernels/norm.py:116 does
+ * with the weight tile it loads.  nkl_rmsnorm is this call with
+ * dtype_w = dtype_in.  Same reference lines as nkl_rmsnorm.
+ */
+int nkl_rmsnorm_ex(const void* x, const void* w, void* y, int rows, int cols,
+                   long ldx, long ldy, float eps, int dtype_in, int dtype_w,
+                   int dtype_out, void* stream);
+
+/*
  * y = silu(g) * u, element-wise over n contiguous elements.
  * Replaces nkilab/kernels/norm.py:121 (swiglu_fused), nkilab/ops.py:65.
  */
 int nkl_swiglu(const void* g, const void* u, void* y, long n, int dtype,
                void* stream);
+
+/*
+ * hi/lo split of an fp32 matrix into bf16: y[r, c] = bf16(x[r, c]) and
+ * y[r, cols + c] = bf16(x[r, c] - y[r, c]) (round-to-nearest-even), so that
+ * hi + lo carries x to 16 significand bits.  A bf16 GEMM over y (K = 2 cols)
+ * against a weight stacked twice along K accumulates x . w in fp32 to about
+ * 2^-17 relative: the decoder block's fp32-accurate projections on bf16 MFMA.
+ * No counterpart in the reference (nkilab/model.py:70-89 runs its block in
+ * one dtype).  x: [rows, cols] fp32 (ldx), y: [rows, 2 cols] bf16 (ldy);
+ * cols, ldx, ldy multiples of 4; x 16-byte, y 8-byte aligned.
+ */
+int nkl_split_bf16(const void* x, void* y, int rows, int cols, long ldx,
+                   long ldy, void* stream);
 
 /*
  * y = x over nbytes (a multiple of 16; both pointers 16-byte aligned): the

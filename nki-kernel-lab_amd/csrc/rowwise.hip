@@ -143,8 +143,30 @@ __global__ __launch_bounds__(256) void softmax_pass3_kernel(const float* __restr
 // ------------------------------------------------------------- RMSNorm --
 // nkilab/kernels/norm.py:92-118: ssq = sum(x^2) (fp32); ms = ssq * (1/D) + eps;
 // rstd = rsqrt(ms); xn = x * rstd (fp32); y = xn * w rounded once.
-template <typename TI, typename TO, int NV>
-__global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const TI* __restrict__ x, const TI* __restrict__ w,
+// E weight elements of type TW (16-byte aligned) as fp32 values.
+template <int E>
+__device__ __forceinline__ void load_w(const float* p, float (&v)[E]) {
+#pragma unroll
+  for (int i = 0; i < E; i += 4) {
+    float t[4];
+    load16(p + i, t);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[i + k] = t[k];
+  }
+}
+template <int E>
+__device__ __forceinline__ void load_w(const bf16* p, float (&v)[E]) {
+  if constexpr (E == 8) {
+    load16(p, v);
+  } else {
+    static_assert(E == 4, "4 or 8 weights per vector");
+    const uint2 t = *reinterpret_cast<const uint2*>(p);
+    v[0] = bf16lo(t.x), v[1] = bf16hi(t.x), v[2] = bf16lo(t.y), v[3] = bf16hi(t.y);
+  }
+}
+
+template <typename TI, typename TW, typename TO, int NV>
+__global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const TI* __restrict__ x, const TW* __restrict__ w,
                                                           TO* __restrict__ y, int rows, int cols, long ldx,
                                                           long ldy, float inv_d, float eps) {
   constexpr int E = VecE<TI>::value;
@@ -175,7 +197,7 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const TI* __restrict__
     const int vi = n * kWave + lane;
     if (vi < nvec) {
       float wv[E];
-      load16(w + (long)vi * E, wv);
+      load_w<E>(w + (long)vi * E, wv);
       float o[E];
 #pragma unroll
       for (int e = 0; e < E; ++e) o[e] = (v[n][e] * rstd) * wv[e];
@@ -184,8 +206,8 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const TI* __restrict__
   }
 }
 
-template <typename TI, typename TO>
-__global__ __launch_bounds__(256) void rmsnorm_loop_kernel(const TI* __restrict__ x, const TI* __restrict__ w,
+template <typename TI, typename TW, typename TO>
+__global__ __launch_bounds__(256) void rmsnorm_loop_kernel(const TI* __restrict__ x, const TW* __restrict__ w,
                                                            TO* __restrict__ y, int rows, int cols, long ldx,
                                                            long ldy, float inv_d, float eps) {
   const int lane = threadIdx.x & 63;
@@ -272,13 +294,13 @@ static int softmax_launch(const void* x, void* y, int rows, int cols, long ldx, 
   return check_launch("nkl_softmax");
 }
 
-template <typename TI, typename TO>
+template <typename TI, typename TW, typename TO>
 static int rmsnorm_launch(const void* x, const void* w, void* y, int rows, int cols, long ldx, long ldy,
                           float eps, hipStream_t st) {
   constexpr int E = VecE<TI>::value;
   const dim3 grid((rows + kRowsPerBlock - 1) / kRowsPerBlock), block(256);
   const TI* xp = static_cast<const TI*>(x);
-  const TI* wp = static_cast<const TI*>(w);
+  const TW* wp = static_cast<const TW*>(w);
   TO* yp = static_cast<TO*>(y);
   // The multiplier 1/D is the fp32 value nearest the exact quotient.
   const float inv_d = (float)(1.0 / (double)cols);
@@ -287,12 +309,12 @@ static int rmsnorm_launch(const void* x, const void* w, void* y, int rows, int c
                    aligned16(w) && aligned16(y);
   const int nv = vec ? pick_nv(cols / E) : 0;
   switch (nv) {
-    case 1: rmsnorm_vec_kernel<TI, TO, 1><<<grid, block, 0, st>>>(xp, wp, yp, rows, cols, ldx, ldy, inv_d, eps); break;
-    case 2: rmsnorm_vec_kernel<TI, TO, 2><<<grid, block, 0, st>>>(xp, wp, yp, rows, cols, ldx, ldy, inv_d, eps); break;
-    case 4: rmsnorm_vec_kernel<TI, TO, 4><<<grid, block, 0, st>>>(xp, wp, yp, rows, cols, ldx, ldy, inv_d, eps); break;
-    case 8: rmsnorm_vec_kernel<TI, TO, 8><<<grid, block, 0, st>>>(xp, wp, yp, rows, cols, ldx, ldy, inv_d, eps); break;
-    case 16: rmsnorm_vec_kernel<TI, TO, 16><<<grid, block, 0, st>>>(xp, wp, yp, rows, cols, ldx, ldy, inv_d, eps); break;
-    default: rmsnorm_loop_kernel<TI, TO><<<grid, block, 0, st>>>(xp, wp, yp, rows, cols, ldx, ldy, inv_d, eps); break;
+    case 1: rmsnorm_vec_kernel<TI, TW, TO, 1><<<grid, block, 0, st>>>(xp, wp, yp, rows, cols, ldx, ldy, inv_d, eps); break;
+    case 2: rmsnorm_vec_kernel<TI, TW, TO, 2><<<grid, block, 0, st>>>(xp, wp, yp, rows, cols, ldx, ldy, inv_d, eps); break;
+    case 4: rmsnorm_vec_kernel<TI, TW, TO, 4><<<grid, block, 0, st>>>(xp, wp, yp, rows, cols, ldx, ldy, inv_d, eps); break;
+    case 8: rmsnorm_vec_kernel<TI, TW, TO, 8><<<grid, block, 0, st>>>(xp, wp, yp, rows, cols, ldx, ldy, inv_d, eps); break;
+    case 16: rmsnorm_vec_kernel<TI, TW, TO, 16><<<grid, block, 0, st>>>(xp, wp, yp, rows, cols, ldx, ldy, inv_d, eps); break;
+    default: rmsnorm_loop_kernel<TI, TW, TO><<<grid, block, 0, st>>>(xp, wp, yp, rows, cols, ldx, ldy, inv_d, eps); break;
   }
   return check_launch("nkl_rmsnorm");
 }
@@ -339,6 +361,31 @@ __global__ __launch_bounds__(256) void stream_copy_kernel(const u32x4* __restric
     const long i = base + k * span;
     if (i < n) __builtin_nontemporal_store(v[k], y + i);
   }
+}
+
+// ------------------------------------------------------ hi/lo bf16 split --
+// y[r, c] = bf16(x[r, c]) and y[r, cols + c] = bf16(x[r, c] - bf16(x[r, c])):
+// an fp32 activation as two bf16 values whose sum carries 16 significand
+// bits.  A GEMM over [hi | lo] (K doubled) against a bf16 weight stacked
+// twice along K then accumulates x . w in fp32 to about 2^-17 of x: the
+// decoder block runs its projections on bf16 MFMA at fp32 accuracy.
+// One thread per 4 consecutive columns of a row (cols % 4 == 0, aligned rows).
+__global__ __launch_bounds__(256) void split_bf16_kernel(const float* __restrict__ x, bf16* __restrict__ y, int rows,
+                                                         int cols, long ldx, long ldy) {
+  const int q = cols / 4;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long)rows * q) return;
+  const int r = (int)(i / q), c = 4 * (int)(i % q);
+  float v[4];
+  load16(x + (long)r * ldx + c, v);
+  float hi[4], lo[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    hi[e] = (float)(bf16)v[e];
+    lo[e] = v[e] - hi[e];  // exact in fp32
+  }
+  store_vec<4>(y + (long)r * ldy + c, hi);
+  store_vec<4>(y + (long)r * ldy + cols + c, lo);
 }
 
 }  // namespace nkl
@@ -398,19 +445,30 @@ extern "C" int nkl_softmax_unfused(const void* x, void* y, void* workspace, size
   return check_launch("nkl_softmax_unfused");
 }
 
-extern "C" int nkl_rmsnorm(const void* x, const void* w, void* y, int rows, int cols, long ldx, long ldy,
-                           float eps, int dtype_in, int dtype_out, void* stream) {
+extern "C" int nkl_rmsnorm_ex(const void* x, const void* w, void* y, int rows, int cols, long ldx, long ldy,
+                              float eps, int dtype_in, int dtype_w, int dtype_out, void* stream) {
   int rc = check_rows("nkl_rmsnorm", rows, cols, ldx, ldy);
   if (rc) return rc;
   if (rows == 0 || cols == 0) return NKL_OK;
+  if (dtype_w != NKL_F32 && dtype_w != NKL_BF16)
+    return set_error(NKL_EDTYPE, "nkl_rmsnorm: unsupported weight dtype %d", dtype_w);
   hipStream_t st = (hipStream_t)stream;
+  const bool wf = dtype_w == NKL_F32;
   if (dtype_in == NKL_F32 && dtype_out == NKL_F32)
-    return rmsnorm_launch<float, float>(x, w, y, rows, cols, ldx, ldy, eps, st);
+    return wf ? rmsnorm_launch<float, float, float>(x, w, y, rows, cols, ldx, ldy, eps, st)
+              : rmsnorm_launch<float, bf16, float>(x, w, y, rows, cols, ldx, ldy, eps, st);
   if (dtype_in == NKL_BF16 && dtype_out == NKL_BF16)
-    return rmsnorm_launch<bf16, bf16>(x, w, y, rows, cols, ldx, ldy, eps, st);
+    return wf ? rmsnorm_launch<bf16, float, bf16>(x, w, y, rows, cols, ldx, ldy, eps, st)
+              : rmsnorm_launch<bf16, bf16, bf16>(x, w, y, rows, cols, ldx, ldy, eps, st);
   if (dtype_in == NKL_F32 && dtype_out == NKL_BF16)
-    return rmsnorm_launch<float, bf16>(x, w, y, rows, cols, ldx, ldy, eps, st);
+    return wf ? rmsnorm_launch<float, float, bf16>(x, w, y, rows, cols, ldx, ldy, eps, st)
+              : rmsnorm_launch<float, bf16, bf16>(x, w, y, rows, cols, ldx, ldy, eps, st);
   return set_error(NKL_EDTYPE, "nkl_rmsnorm: unsupported dtype pair (%d -> %d)", dtype_in, dtype_out);
+}
+
+extern "C" int nkl_rmsnorm(const void* x, const void* w, void* y, int rows, int cols, long ldx, long ldy,
+                           float eps, int dtype_in, int dtype_out, void* stream) {
+  return nkl_rmsnorm_ex(x, w, y, rows, cols, ldx, ldy, eps, dtype_in, dtype_in, dtype_out, stream);
 }
 
 extern "C" int nkl_swiglu(const void* g, const void* u, void* y, long n, int dtype, void* stream) {
@@ -434,4 +492,17 @@ extern "C" int nkl_stream_copy(const void* x, void* y, long nbytes, void* stream
   stream_copy_kernel<<<dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream>>>(static_cast<const u32x4*>(x),
                                                                                    static_cast<u32x4*>(y), n);
   return check_launch("nkl_stream_copy");
+}
+
+extern "C" int nkl_split_bf16(const void* x, void* y, int rows, int cols, long ldx, long ldy, void* stream) {
+  if (rows < 0 || cols < 0) return set_error(NKL_EINVAL, "nkl_split_bf16: negative shape (%d, %d)", rows, cols);
+  if (rows == 0 || cols == 0) return NKL_OK;
+  if (cols % 4 || ldx % 4 || ldy % 4 || ldx < cols || ldy < 2L * cols || ((uintptr_t)x & 15u) || ((uintptr_t)y & 7u))
+    return set_error(NKL_EINVAL,
+                     "nkl_split_bf16: cols %d and leading dimensions (%ld, %ld) must be multiples of 4 with "
+                     "ldx >= cols, ldy >= 2 cols; x 16-byte and y 8-byte aligned", cols, ldx, ldy);
+  const long n = (long)rows * (cols / 4);
+  split_bf16_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream>>>(
+      static_cast<const float*>(x), static_cast<bf16*>(y), rows, cols, ldx, ldy);
+  return check_launch("nkl_split_bf16");
 }

@@ -30,8 +30,11 @@ SIGNATURES = {
     "nkl_softmax_unfused_workspace_bytes": (_c_size, [_c_int, _c_int]),
     "nkl_softmax_unfused": (_c_int, [_vp, _vp, _vp, _c_size, _c_int, _c_int, _c_long, _c_long, _c_int, _vp]),
     "nkl_rmsnorm": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_long, _c_long, _c_float, _c_int, _c_int, _vp]),
+    "nkl_rmsnorm_ex": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_long, _c_long, _c_float, _c_int, _c_int, _c_int,
+                                _vp]),
     "nkl_swiglu": (_c_int, [_vp, _vp, _vp, _c_long, _c_int, _vp]),
     "nkl_stream_copy": (_c_int, [_vp, _vp, _c_long, _vp]),
+    "nkl_split_bf16": (_c_int, [_vp, _vp, _c_int, _c_int, _c_long, _c_long, _vp]),
     "nkl_flash_attn_causal": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_long, _c_long, _c_long,
                                        _c_long, _c_long, _c_long, _c_long, _c_long, _c_float, _c_int, _vp]),
     "nkl_flash_attn_causal_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int]),

@@ -64,8 +64,21 @@ def _row_major(t: torch.Tensor, cols: int) -> tuple[torch.Tensor, int]:
 
 def _gemm(a: torch.Tensor, bmat: torch.Tensor, ldb: int, b_trans: bool, c: torch.Tensor,
           residual: torch.Tensor | None, variant: str) -> torch.Tensor:
+    # The C ABI takes bare pointers and sizes: every shape is checked here, so
+    # that a mismatch raises instead of reading or writing past a buffer.
+    if a.dim() != 2 or bmat.dim() != 2 or c.dim() != 2:
+        raise ValueError(f"gemm: 2-D operands expected, got {tuple(a.shape)}, {tuple(bmat.shape)}, {tuple(c.shape)}")
     M, K = a.shape
     N = c.shape[1]
+    if c.shape[0] != M:
+        raise ValueError(f"gemm: output {tuple(c.shape)} does not have the {M} rows of a {tuple(a.shape)}")
+    want_b = (N, K) if b_trans else (K, N)
+    if tuple(bmat.shape) != want_b:
+        raise ValueError(f"gemm: b {tuple(bmat.shape)} does not match [{'N, K' if b_trans else 'K, N'}] = {want_b}")
+    if residual is not None and tuple(residual.shape) != (M, N):
+        raise ValueError(f"gemm: residual {tuple(residual.shape)} does not match the output [{M}, {N}]")
+    if a.dtype != bmat.dtype:
+        raise TypeError(f"gemm: a and b must share a dtype, got {a.dtype} and {bmat.dtype}")
     a, lda = _row_major(a, K)
     if c.dim() != 2 or (c.stride(1) != 1 and N > 1) or (M > 1 and c.stride(0) < N):
         raise ValueError("gemm: the output must be a row-major [M, N] tensor")
@@ -126,6 +139,8 @@ def gemm_swiglu_into(a: torch.Tensor, w_gu: torch.Tensor, c: torch.Tensor) -> to
     [2N, K] and c [M, N].  Equal to two bf16 linear_into calls and swiglu_into."""
     M, K = a.shape
     N = c.shape[1]
+    if c.shape[0] != M:
+        raise ValueError(f"gemm_swiglu_into: output {tuple(c.shape)} does not have the {M} rows of a")
     if w_gu.shape != (2 * N, K):
         raise ValueError(f"gemm_swiglu_into: packed weight {tuple(w_gu.shape)} does not match [2*{N}, {K}]")
     if not (a.dtype == w_gu.dtype == c.dtype == torch.bfloat16):
@@ -155,6 +170,28 @@ def matmul(a, b, variant: str = "blocked"):
     c = torch.empty((M, N), dtype=ta.dtype, device=ta.device)
     gemm_into(ta, tb, c, variant=variant)
     return from_device(c, kind)
+
+
+def split_bf16_into(x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+    """y[:, :K] = bf16(x), y[:, K:] = bf16(x - y[:, :K]) for an fp32 x [M, K] and a
+    bf16 y [M, 2K]: the hi/lo pair a bf16 GEMM against ``stack_k(w)``
+    multiplies with fp32 accuracy."""
+    if x.dim() != 2 or y.dim() != 2 or y.shape != (x.shape[0], 2 * x.shape[1]):
+        raise ValueError(f"split_bf16_into: y {tuple(y.shape)} must be [M, 2K] for x {tuple(x.shape)}")
+    if x.dtype != torch.float32 or y.dtype != torch.bfloat16:
+        raise TypeError("split_bf16_into: fp32 x and bf16 y expected")
+    M, K = x.shape
+    x2, _, _, ldx = _as_rows(x)
+    if y.stride(1) != 1:
+        raise ValueError("split_bf16_into: y must have unit column stride")
+    _lib.call("nkl_split_bf16", ptr(x2), ptr(y), M, K, ldx, y.stride(0) if M > 1 else 2 * K, stream_handle())
+    return y
+
+
+def stack_k(w: torch.Tensor) -> torch.Tensor:
+    """[w | w] along K for an nn.Linear weight w [N, K] (bf16): the B operand
+    that pairs with split_bf16_into's [hi | lo] activations."""
+    return torch.cat((w, w), dim=1).contiguous()
 
 
 # ---------------------------------------------------------------- RoPE --
@@ -194,6 +231,8 @@ def _as_rows(t: torch.Tensor) -> tuple[torch.Tensor, int, int, int]:
 
 
 def softmax_into(x: torch.Tensor, y: torch.Tensor, fused: bool = True) -> torch.Tensor:
+    if y.shape != x.shape or y.dtype != x.dtype:
+        raise ValueError(f"softmax_into: y {tuple(y.shape)} {y.dtype} must match x {tuple(x.shape)} {x.dtype}")
     x2, R, D, ldx = _as_rows(x)
     y2, _, _, ldy = _as_rows(y)
     dt = dtype_code(x2.dtype)
@@ -217,15 +256,21 @@ def softmax(x, fused: bool = True):
 
 
 def rmsnorm_into(x: torch.Tensor, weight: torch.Tensor, y: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
-    """y = x * rsqrt(mean(x^2) + eps) * weight; weight has x's dtype, y may be
-    bf16 for an fp32 x."""
+    """y = x * rsqrt(mean(x^2) + eps) * weight.  The normalised row stays in
+    fp32 and is multiplied by the weight in the weight's own dtype (fp32 or
+    bf16, independent of x's), then rounded once to y's dtype (x's, or bf16
+    for an fp32 x)."""
+    if y.shape != x.shape:
+        raise ValueError(f"rmsnorm_into: y {tuple(y.shape)} must match x {tuple(x.shape)}")
     x2, R, D, ldx = _as_rows(x)
+    if weight.numel() != D:
+        raise ValueError(f"rmsnorm_into: weight has {weight.numel()} elements, x rows have {D}")
     if y.stride(-1) != 1 or not y.is_contiguous():
         raise ValueError("rmsnorm_into: output must be contiguous")
     y2 = y.view(R, D)
     w = weight.contiguous()
-    _lib.call("nkl_rmsnorm", ptr(x2), ptr(w), ptr(y2), R, D, ldx, D, float(eps), dtype_code(x2.dtype),
-              dtype_code(y2.dtype), stream_handle())
+    _lib.call("nkl_rmsnorm_ex", ptr(x2), ptr(w), ptr(y2), R, D, ldx, D, float(eps), dtype_code(x2.dtype),
+              dtype_code(w.dtype), dtype_code(y2.dtype), stream_handle())
     return y
 
 
@@ -233,12 +278,16 @@ def rmsnorm(x, weight, eps: float = 1e-6):
     """y = x * rsqrt(mean(x^2, -1) + eps) * weight (ops.py:60-61)."""
     t, kind = to_device(x)
     w, _ = to_device(weight)
-    w = w.to(t.dtype)
     y = torch.empty(t.shape, dtype=t.dtype, device=t.device)
     return from_device(rmsnorm_into(t, w, y, eps), kind)
 
 
 def swiglu_into(gate: torch.Tensor, up: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+    if up.shape != gate.shape or y.shape != gate.shape:
+        raise ValueError(f"swiglu_into: gate {tuple(gate.shape)}, up {tuple(up.shape)} and y {tuple(y.shape)} "
+                         "must have one shape")
+    if not (gate.dtype == up.dtype == y.dtype):
+        raise TypeError(f"swiglu_into: gate, up and y must share a dtype, got {gate.dtype}, {up.dtype}, {y.dtype}")
     g, u = gate.contiguous(), up.contiguous()
     if not y.is_contiguous():
         raise ValueError("swiglu_into: output must be contiguous")
@@ -285,16 +334,23 @@ ATTENTION_VARIANTS = {
 # workspace (no initialisation needed) and an arrival-counter array zeroed
 # once, which the kernel leaves at zero after every call.  Calls on one stream
 # run one after another, so they can share both.  Each is grown when a call
-# needs more (the counters are then re-zeroed).
+# needs more (the counters are then re-zeroed).  Buffers a call has used are
+# never freed: a captured HIP graph may still replay launches that point at
+# them, so outgrown ones are kept for the life of the process.
 _FLASH_SCRATCH: dict = {}
+_FLASH_RETIRED: list = []
 
 
 def _flash_scratch(ws_bytes: int, counter_bytes: int, dev: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
     key = (dev, stream_handle())
     ws, cnt = _FLASH_SCRATCH.get(key, (None, None))
     if ws is None or ws.numel() < ws_bytes:
+        if ws is not None:
+            _FLASH_RETIRED.append(ws)
         ws = torch.empty(max(ws_bytes, 1 << 20), dtype=torch.uint8, device=dev)
     if cnt is None or cnt.numel() * 4 < counter_bytes:
+        if cnt is not None:
+            _FLASH_RETIRED.append(cnt)
         cnt = torch.zeros(max(counter_bytes // 4, 4096), dtype=torch.int32, device=dev)
     _FLASH_SCRATCH[key] = (ws, cnt)
     return ws, cnt
@@ -317,6 +373,9 @@ def attention_into(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.T
     if k.shape != v.shape or k.shape[1:] != q.shape[1:] or Hkv < 1 or H % Hkv:
         raise ValueError(f"attention_into: k, v {tuple(k.shape)}, {tuple(v.shape)} must be [Hkv, S, d] with Hkv "
                          f"dividing the {H} query heads of q {tuple(q.shape)}")
+    if o.shape != q.shape or o.dtype != q.dtype or not (q.dtype == k.dtype == v.dtype):
+        raise ValueError(f"attention_into: o {tuple(o.shape)} {o.dtype} must match q {tuple(q.shape)} {q.dtype}, "
+                         "and k, v share q's dtype")
     if scale is None:
         scale = 1.0 / math.sqrt(d)
     E = 8 if q.dtype == torch.bfloat16 else 4

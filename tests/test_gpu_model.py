@@ -73,6 +73,60 @@ def test_decoder_block_2048_hidden_config():
     assert err <= 1e-3, err
 
 
+def test_decoder_block_2048_hidden_split_operands():
+    """The timed configuration: fp32 activations and residual, every projection on
+    bf16 MFMA over hi/lo operand pairs against K-stacked bf16 weights, fp32
+    attention -- max relative error <= 1e-3 against the fp32 block."""
+    from nkilab import workloads
+    from nkilab.model import nki_forward
+
+    block, x = workloads.decoder_inputs()
+    block = block.cuda()
+    xg = x.cuda()
+    with torch.no_grad():
+        ref = block(xg).cpu().numpy()
+    out = nki_forward(block, xg, compute_dtype="split")
+    assert out.dtype == torch.float32 and out.is_cuda
+    err = rel_err(out.cpu().numpy(), ref)
+    assert err <= 1e-3, err
+
+
+@pytest.mark.parametrize("S", [64, 300])
+def test_decoder_split_small_block_matches_pytorch(S):
+    """A small block with bf16-valued weights and uniform(0.5, 1.5) norm weights
+    under the split policy, against the fp32 eager block; and a block whose
+    weights are not bf16 numbers, which takes the fp32 GEMM for them."""
+    from nkilab.model import BlockConfig, DecoderBlock, nki_forward
+
+    torch.manual_seed(5)
+    block = DecoderBlock(BlockConfig(d_model=128, n_heads=2, d_ff=256)).eval()
+    with torch.no_grad():
+        for n in ("wqkv", "wo", "wg", "wu", "wd"):
+            w = getattr(block, n).weight
+            w.copy_(w.bfloat16().float())
+    x = torch.randn(S, 128)
+    with torch.no_grad():
+        ref = block(x).numpy()
+    out = nki_forward(block, x.numpy(), compute_dtype="split")
+    assert rel_err(out, ref) <= 1e-4
+    with torch.no_grad():
+        block.wo.weight.add_(1e-4)  # no longer bf16 numbers
+        ref2 = block(x).numpy()
+    assert rel_err(nki_forward(block, x.numpy(), compute_dtype="split"), ref2) <= 1e-4
+
+
+def test_split_bf16_pairs(rng):
+    """hi is x rounded to bf16 exactly; hi + lo carries x to 2^-16 relative."""
+    from nkilab import ops
+
+    x = torch.from_numpy((rng.standard_normal((37, 96)) * 10.0 ** rng.uniform(-3, 3, (37, 96))).astype(np.float32)).cuda()
+    y = torch.empty((37, 192), dtype=torch.bfloat16, device="cuda")
+    ops.split_bf16_into(x, y)
+    hi, lo = y[:, :96].float(), y[:, 96:].float()
+    assert torch.equal(hi, x.bfloat16().float())
+    assert float(((hi + lo - x).abs() / x.abs().clamp_min(1e-30)).max()) <= 2.0 ** -16
+
+
 def test_decoder_block_2048_hidden_bf16_activations():
     """The same block with bf16 GEMM / attention operands and an fp32 residual stream.
     Its error against the fp32 block is set by bf16 rounding of the activations (a CPU

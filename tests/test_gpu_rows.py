@@ -75,6 +75,24 @@ def test_rmsnorm_bf16(rng):
     assert rel_err(_np(out), ref) < 1e-2
 
 
+@pytest.mark.parametrize("R,D", [(64, 2048), (33, 520), (5, 77)])
+def test_rmsnorm_bf16_activations_fp32_weight(rng, R, D):
+    """bf16 x with an fp32 weight: the fp32 normalised row is multiplied by the
+    fp32 weight and rounded once (norm.py:116), as the oracle does -- not by a
+    weight first rounded to bf16."""
+    from nkilab import ops
+
+    x = _bf(rng.standard_normal((R, D)))
+    w = torch.from_numpy(rng.uniform(0.5, 1.5, D).astype(np.float32)).cuda()
+    out = ops.rmsnorm(x, w)
+    assert out.dtype == torch.bfloat16
+    ref = O.rmsnorm_fused(_np(x), w.cpu().numpy(), 1e-6, O.BF16)
+    assert_within_bf16_ulps(_np(out), ref, 1.0, 1e-6)
+    # rounding the weight to bf16 first gives a different result on some elements
+    coarse = O.rmsnorm_fused(_np(x), O.bf16_round(w.cpu().numpy()), 1e-6, O.BF16)
+    assert np.abs(ref - coarse).max() > 0
+
+
 def test_swiglu_matches_torch(rng):
     from nkilab import ops
 

@@ -239,3 +239,42 @@ def test_decoder_block_eager_matches_closed_form():
     gate = hh @ W["wg"].T
     ref = x1 + ((gate / (1 + np.exp(-gate))) * (hh @ W["wu"].T)) @ W["wd"].T
     np.testing.assert_allclose(y, ref, atol=1e-5)
+
+
+def test_ops_reject_mismatched_operands_before_launching():
+    """The C ABI takes bare pointers and sizes, so the Python layer checks every
+    operand against the others and raises before any launch (CPU tensors: a
+    launch would fail differently)."""
+    import torch
+
+    from nkilab import ops
+
+    x = torch.zeros(4, 8)
+    with pytest.raises(ValueError):
+        ops.rmsnorm_into(x, torch.zeros(7), torch.empty(4, 8))      # weight length != D
+    with pytest.raises(ValueError):
+        ops.rmsnorm_into(x, torch.zeros(8), torch.empty(4, 7))      # y shape != x shape
+    with pytest.raises(ValueError):
+        ops.softmax_into(x, torch.empty(4, 7))
+    with pytest.raises(ValueError):
+        ops.swiglu_into(x, torch.zeros(4, 7), torch.empty(4, 8))    # up shape != gate shape
+    with pytest.raises(ValueError):
+        ops.swiglu_into(x, x, torch.empty(3, 8))                    # y shape != gate shape
+    with pytest.raises(TypeError):
+        ops.swiglu_into(x, x.bfloat16(), torch.empty(4, 8))
+    q = torch.zeros(2, 16, 8)
+    with pytest.raises(ValueError):
+        ops.attention_into(q, q, q, torch.empty(2, 16, 4))          # o shape != q shape
+    with pytest.raises(ValueError):
+        ops.attention_into(q, q, q, torch.empty(2, 16, 8, dtype=torch.bfloat16))
+    a = torch.zeros(4, 8)
+    with pytest.raises(ValueError):
+        ops.gemm_into(a, torch.zeros(8, 5), torch.empty(4, 6))      # c columns != b columns
+    with pytest.raises(ValueError):
+        ops.gemm_into(a, torch.zeros(8, 5), torch.empty(3, 5))      # c rows != a rows
+    with pytest.raises(ValueError):
+        ops.gemm_into(a, torch.zeros(7, 5), torch.empty(4, 5))      # b rows != a columns
+    with pytest.raises(ValueError):
+        ops.linear_into(a, torch.zeros(5, 7), torch.empty(4, 5))    # weight [N, K] with K != 8
+    with pytest.raises(ValueError):
+        ops.linear_into(a, torch.zeros(5, 8), torch.empty(4, 5), residual=torch.zeros(4, 4))
