@@ -1,12 +1,15 @@
 """Measured throughput of the kernel set on one MI355X, next to the CPU path.
 
-    python bench.py [--steps K] [--warmup W] [--all] [--report FILE]
+    python bench.py [--steps K] [--warmup W] [--report FILE] [--gemm-shapes]
+    python bench.py --collect-counters OUT    (rocprofv3 counter passes -> profiles/counters.json)
 
 Prints ONE JSON line.  The headline (``value``) is causal attention at
 8 heads x 2048 x d128 bf16 in TFLOP/s, counting the exact causal FLOPs
-4*H*d*S(S+1)/2; the fused softmax / RMSNorm / SwiGLU at 4096 x 2048 bf16 are
-reported in the same line as HBM GB/s and fraction of peak.  ``--all`` adds
-the 1024^3 GEMM, the long-context attention configs and the decoder block.
+4*H*d*S(S+1)/2.  The same line carries every other benchmark configuration,
+each with its own roofline object: the fused softmax / RMSNorm / SwiGLU at
+4096 x 2048 bf16 (HBM GB/s), the 1024^3 bf16 matmul, causal attention at
+1 x 4096 and 32 x 16384, and the decoder block (the configuration that meets
+1e-3 against the fp32 block, with the all-bf16 one beside it).
 
 Timing: every kernel is launched from a captured HIP graph (so host launch
 overhead does not leave the GPU idle between launches), replayed K times
@@ -45,7 +48,10 @@ def log(msg: str) -> None:
 def time_launches(launches, reps: int, warmup: int) -> float:
     """Seconds per launch: capture `launches` (zero-arg callables, one kernel
     each) into a HIP graph, replay it `warmup` times, then `reps` times between
-    two events on the current stream."""
+    two events on the current stream.  The eager warm-up runs on the stream
+    the capture uses, so that per-stream scratch (the attention's partial
+    states and counters) exists before capture and no allocation or fill is
+    captured into the timed graph."""
     import torch
 
     side = torch.cuda.Stream()
@@ -56,7 +62,7 @@ def time_launches(launches, reps: int, warmup: int) -> float:
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.cuda.graph(graph, stream=side):
         for f in launches:
             f()
     for _ in range(warmup):
@@ -76,10 +82,17 @@ def n_sets(bytes_per_set: int) -> int:
     return max(2, math.ceil(2 * LLC_BYTES / bytes_per_set))
 
 
-def roofline(bound: str, achieved: float, unit: str, traffic=None) -> dict:
+def roofline(bound: str, achieved: float, unit: str, counters: dict | None = None) -> dict:
+    """The roofline object of one workload; `counters` is its entry of
+    profiles/counters.json (HBM bytes per launch from FETCH_SIZE/WRITE_SIZE,
+    MFMA busy fraction from SQ_VALU_MFMA_BUSY_CYCLES), when collected."""
     peak = PEAK_BF16_TFLOPS if bound == "mfma" else PEAK_HBM_GBS
-    return {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
-            "frac": round(achieved / peak, 4), "traffic": traffic}
+    c = counters or {}
+    out = {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
+           "frac": round(achieved / peak, 4), "traffic": c.get("bytes")}
+    if bound == "mfma":
+        out["mfma_busy"] = c.get("mfma_busy")
+    return out
 
 
 # ------------------------------------------------------------ workloads --
@@ -89,8 +102,6 @@ def bench_attention(H, S, d, reps, warmup, seed=0, sets=None):
 
     from nkilab import ops, workloads
 
-    import oracle as O  # noqa: F401  (flop count only)
-
     q, k, v = (t.cuda() for t in workloads.attention_inputs(H, S, d, seed=seed))
     per_set = 4 * H * S * d * 2
     sets = sets or min(n_sets(per_set), 16)
@@ -98,7 +109,7 @@ def bench_attention(H, S, d, reps, warmup, seed=0, sets=None):
         (q.clone(), k.clone(), v.clone(), torch.empty_like(q)) for _ in range(sets - 1)]
     launches = [lambda b=b: ops.attention_into(*b) for b in bufs]
     sec = time_launches(launches, reps, warmup)
-    flops = O.causal_flops(H, S, d)
+    flops = workloads.causal_flops(H, S, d)
     return {"H": H, "S": S, "d": d, "us": sec * 1e6, "tflops": flops / sec / 1e12, "flops": flops,
             "bytes": per_set, "buffer_sets": sets}, bufs[0]
 
@@ -207,7 +218,10 @@ def bench_gemm_shapes(reps, warmup):
     return out
 
 
-def bench_decoder(reps, warmup):
+def bench_decoder(reps, warmup, counters=None):
+    """The decoder block (config 5): the split-operand configuration, which
+    meets 1e-3 against the fp32 block and is the one reported, and the
+    all-bf16 configuration beside it; each with its measured error."""
     import torch
 
     from nkilab import workloads
@@ -216,18 +230,26 @@ def bench_decoder(reps, warmup):
     block, x = workloads.decoder_inputs()
     block = block.cuda()
     xg = x.cuda()
-    nki_forward(block, xg, compute_dtype="bfloat16")  # fills the weight cache and the attention scratch
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        nki_forward(block, xg, compute_dtype="bfloat16")
-    torch.cuda.synchronize()
-    eager = (time.perf_counter() - t0) / reps
-    sec = time_launches([lambda: nki_forward(block, xg, compute_dtype="bfloat16")], reps, warmup)
-    flops = 227_641_655_296
-    return {"us": sec * 1e6, "tflops": flops / sec / 1e12, "frac": flops / sec / 1e12 / PEAK_BF16_TFLOPS,
-            "eager_us": eager * 1e6,
-            "note": "7 launches per block (2 RMSNorm, QKV, attention, out-proj, fused gate/up/SwiGLU, down-proj) replayed from a HIP graph; eager_us is the Python loop's wall clock"}
+    with torch.no_grad():
+        ref = block(xg)
+    flops = workloads.decoder_flops()
+    out = {}
+    for name, cd, launches in (("split", "split", "13 launches: 2 RMSNorm, 4 hi/lo splits, 5 bf16 GEMMs over K-doubled "
+                                                  "operands, fp32 attention, SwiGLU"),
+                               ("bf16", "bfloat16", "7 launches: 2 RMSNorm, QKV, attention, out-proj, fused "
+                                                    "gate/up/SwiGLU, down-proj")):
+        y = nki_forward(block, xg, compute_dtype=cd)  # fills the weight cache and the attention scratch
+        torch.cuda.synchronize()
+        err = float((y.float() - ref).abs().max() / ref.abs().max())
+        sec = time_launches([lambda cd=cd: nki_forward(block, xg, compute_dtype=cd)], reps, warmup)
+        out[name] = {"us": round(sec * 1e6, 3), "tflops": round(flops / sec / 1e12, 3),
+                     "rel_err_vs_fp32_block": err, "launches": launches}
+    rep = out["split"]
+    return {"us": rep["us"], "tflops": rep["tflops"], "rel_err_vs_fp32_block": rep["rel_err_vs_fp32_block"],
+            "compute": "split: fp32 activations and residual, projections on bf16 MFMA over hi/lo operand pairs, "
+                       "fp32 attention",
+            "roofline": roofline("mfma", rep["tflops"], "TFLOP/s", (counters or {}).get("decoder")),
+            "flops_per_step": flops, "bf16_activations": out["bf16"], "split_detail": out["split"]}
 
 
 # ---------------------------------------------------------- CPU baseline --
@@ -239,9 +261,11 @@ def cpu_baseline(q, k, v, gpu_out):
 
     import oracle as O
 
+    from nkilab import workloads
+
     H, S, d = q.shape
     qn, kn, vn = (t.float().cpu().numpy() for t in (q, k, v))
-    flops = O.causal_flops(H, S, d)
+    flops = workloads.causal_flops(H, S, d)
     try:
         from threadpoolctl import threadpool_info
         blas_threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
@@ -355,28 +379,37 @@ def cpu_rows_baseline(ncores: int) -> dict:
     return out
 
 
-# --------------------------------------------------------- HBM traffic --
+# -------------------------------------------------------- counters --
 #
-# `traffic` in the roofline objects is HBM bytes per launch from two
-# rocprofv3 counter passes, FETCH_SIZE then WRITE_SIZE (KiB per dispatch),
-# each scaled by what the same counter reads for a plain streaming kernel
-# (torch.neg over 256 MiB of fp32: one read and one write of known size) in
-# the same pass:
-#   rocprofv3 --pmc FETCH_SIZE -d OUT -o fetch -f csv -- python3 bench.py --pmc-pass
-#   rocprofv3 --pmc WRITE_SIZE -d OUT -o write -f csv -- python3 bench.py --pmc-pass
-#   python bench.py --parse-traffic OUT/.../fetch_counter_collection.csv OUT/.../write_counter_collection.csv
-# The last step writes profiles/hbm_traffic.json, which later runs report.
+# profiles/counters.json holds, per workload, what rocprofv3 counters read for
+# its kernels: HBM bytes per launch (FETCH_SIZE, then WRITE_SIZE, in KiB per
+# dispatch, each scaled by what the same counter reads per byte for a plain
+# streaming kernel -- torch.neg over 256 MiB of fp32 -- in the same run) and
+# the MFMA busy fraction
+#     mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (4 * CUs * GRBM_GUI_ACTIVE / XCDs)
+# (MFMA-busy SIMD-cycles over the SIMD-cycles of the dispatch; GRBM_GUI_ACTIVE
+# sums the busy cycles of the XCDs' command front ends), next to the FLOPs the
+# MFMAs issued, SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512.  Written by
+#     python bench.py --collect-counters OUT
+# which runs one rocprofv3 pass per workload and counter set over
+# `bench.py --pmc-pass WORKLOAD` (eager launches on cold buffers).
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+COUNTERS_FILE = os.path.join(ROOT, "profiles", "counters.json")
 COPY_BYTES = 256 << 20
-KERNEL_KEYS = {"attention": "flash_bf16_kernel", "softmax": "softmax_vec_kernel",
-               "rmsnorm": "rmsnorm_vec_kernel", "swiglu": "swiglu_vec_kernel", "copy": "neg_kernel"}
+COUNTER_SETS = {"fetch": ["FETCH_SIZE"], "write": ["WRITE_SIZE"],
+                "mfma": ["SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CU_CYCLES",
+                         "GRBM_GUI_ACTIVE"]}
+# workload -> kernel-name substring of its dominant kernel ("" = every kernel
+# of the workload but the calibration copy)
+PMC_WORKLOADS = {"attention": "flash", "attention_1x4096": "flash", "attention_32x16384": "flash",
+                 "matmul": "gemm", "softmax": "softmax_vec", "rmsnorm": "rmsnorm_vec", "swiglu": "swiglu_vec",
+                 "decoder": ""}
+PMC_REPS = 8
 
 
-def pmc_pass() -> None:
-    """Eager launches for the counter passes: the calibration copy, then each
-    benchmark kernel on rotating buffer sets (cold last-level cache, as in the
-    timed runs)."""
+def pmc_pass(workload: str) -> None:
+    """Eager launches for one counter pass: the calibration copy, then the
+    workload PMC_REPS times on rotating buffer sets (cold last-level cache)."""
     import torch
 
     from nkilab import ops, workloads
@@ -385,60 +418,130 @@ def pmc_pass() -> None:
     dst = torch.empty_like(src)
     for _ in range(3):
         torch.neg(src, out=dst)  # one streaming read and write of COPY_BYTES each
-    del src, dst
-    q, k, v = (t.cuda() for t in workloads.attention_inputs())
-    sets = [(q.clone(), k.clone(), v.clone(), torch.empty_like(q)) for _ in range(16)]
-    for b in sets:
-        ops.attention_into(*b)
-    del sets
-    x, w, gate, up = (t.cuda() for t in workloads.rows_inputs(4096, 2048))
-    xs = [(x.clone(), torch.empty_like(x)) for _ in range(16)]
-    for b in xs:
-        ops.softmax_into(*b)
-    for b in xs:
-        ops.rmsnorm_into(b[0], w, b[1], 1e-6)
-    del xs
-    gs = [(gate.clone(), up.clone(), torch.empty_like(gate)) for _ in range(11)]
-    for b in gs:
-        ops.swiglu_into(*b)
     torch.cuda.synchronize()
-    log("pmc pass done")
+    del src, dst
+    if workload.startswith("attention"):
+        H, S = {"attention": (8, 2048), "attention_1x4096": (1, 4096), "attention_32x16384": (32, 16384)}[workload]
+        q, k, v = (t.cuda() for t in workloads.attention_inputs(H, S, 128))
+        n = 2 if S > 8192 else PMC_REPS
+        sets = [(q.clone(), k.clone(), v.clone(), torch.empty_like(q)) for _ in range(2 if S > 8192 else 16)]
+        for i in range(n):
+            ops.attention_into(*sets[i % len(sets)])
+    elif workload == "matmul":
+        a, b = (t.cuda() for t in workloads.matmul_inputs())
+        sets = [(a.clone(), b.clone(), torch.empty_like(a)) for _ in range(64)]
+        for i in range(PMC_REPS):
+            ops.gemm_into(*sets[i])
+    elif workload in ("softmax", "rmsnorm", "swiglu"):
+        x, w, gate, up = (t.cuda() for t in workloads.rows_inputs(4096, 2048))
+        for i in range(PMC_REPS):
+            if workload == "softmax":
+                ops.softmax_into(x.clone(), torch.empty_like(x))
+            elif workload == "rmsnorm":
+                ops.rmsnorm_into(x.clone(), w, torch.empty_like(x), 1e-6)
+            else:
+                ops.swiglu_into(gate.clone(), up.clone(), torch.empty_like(gate))
+    elif workload == "decoder":
+        from nkilab.model import nki_forward
+
+        block, x = workloads.decoder_inputs()
+        block, xg = block.cuda(), x.cuda()
+        for _ in range(2):
+            nki_forward(block, xg, compute_dtype="split")
+    else:
+        raise SystemExit(f"unknown counter workload {workload!r}; one of {sorted(PMC_WORKLOADS)}")
+    torch.cuda.synchronize()
+    log(f"pmc pass {workload} done")
 
 
-def _counter_means(path: str) -> dict:
-    import csv
+def collect_counters(out_dir: str) -> dict:
+    """Every counter pass of every workload under rocprofv3 (one child process
+    each, under `timeout -s KILL`), then profiles/counters.json from them."""
+    import glob
+    import subprocess
 
-    sums: dict = {}
-    with open(path) as f:
-        for row in csv.DictReader(f):
-            name = row.get("Kernel_Name") or row.get("Kernel-Name") or ""
-            val = float(row.get("Counter_Value") or row.get("Counter-Value") or 0.0)
-            for key, pat in KERNEL_KEYS.items():
-                if pat in name:
-                    n, tot = sums.get(key, (0, 0.0))
-                    sums[key] = (n + 1, tot + val)
-    return {k: tot / n for k, (n, tot) in sums.items()}
-
-
-def parse_traffic(fetch_csv: str, write_csv: str) -> dict:
-    fetch, write = _counter_means(fetch_csv), _counter_means(write_csv)
-    f_copy = fetch["copy"] * 1024 / COPY_BYTES   # counter bytes per real byte read
-    w_copy = write["copy"] * 1024 / COPY_BYTES   # counter bytes per real byte written
-    out = {"calibration": {"copy_bytes": COPY_BYTES, "fetch_kib": fetch["copy"], "write_kib": write["copy"],
-                           "fetch_factor": f_copy, "write_factor": w_copy},
-           "source": [os.path.basename(fetch_csv), os.path.basename(write_csv)]}
-    for key in ("attention", "softmax", "rmsnorm", "swiglu"):
-        if key in fetch and key in write:
-            rd = fetch[key] * 1024 / f_copy
-            wr = write[key] * 1024 / w_copy
-            out[key] = {"fetch_kib": fetch[key], "write_kib": write[key], "read_bytes": round(rd),
-                        "write_bytes": round(wr), "bytes": round(rd + wr)}
+    out_dir = os.path.abspath(out_dir)
+    env = dict(os.environ, TMPDIR="/tmp")
+    for wl in PMC_WORKLOADS:
+        for tag, ctrs in COUNTER_SETS.items():
+            d = os.path.join(out_dir, f"{wl}_{tag}")
+            cmd = ["timeout", "-s", "KILL", "180", "rocprofv3", "--pmc", *ctrs, "-d", d, "-o", "c", "-f", "csv", "--",
+                   sys.executable, os.path.abspath(__file__), "--pmc-pass", wl]
+            log(f"counters: {wl} {tag}")
+            r = subprocess.run(cmd, cwd="/tmp", env=env, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+            if r.returncode != 0 or not glob.glob(os.path.join(d, "**", "c_counter_collection.csv"), recursive=True):
+                raise SystemExit(f"rocprofv3 pass {wl}/{tag} failed ({r.returncode}):\n{r.stdout[-3000:]}")
+    out = parse_counters(out_dir)
+    for path in (COUNTERS_FILE, os.path.join(out_dir, "counters.json")):
+        with open(path, "w") as f:
+            json.dump(out, f, indent=1)
     return out
 
 
-def load_traffic() -> dict:
+def _rows(path: str):
+    import csv
+
+    with open(path) as f:
+        for row in csv.DictReader(f):
+            yield (row.get("Kernel_Name") or row.get("Kernel-Name") or "", row.get("Counter_Name", ""),
+                   float(row.get("Counter_Value") or 0.0), int(row.get("Dispatch_Id") or 0))
+
+
+def parse_counters(out_dir: str) -> dict:
+    """profiles/counters.json from the CSVs of collect_counters()."""
+    import glob
+
+    def csv_of(wl, tag):
+        return glob.glob(os.path.join(out_dir, f"{wl}_{tag}", "**", "c_counter_collection.csv"), recursive=True)[0]
+
+    res = {"formula": {"traffic": "FETCH_SIZE and WRITE_SIZE (KiB per dispatch) over the same counter's KiB per "
+                                  "byte for torch.neg over 256 MiB of fp32 in the same run",
+                       "mfma_busy": "SQ_VALU_MFMA_BUSY_CYCLES / (4 * CUs * GRBM_GUI_ACTIVE / XCDs)",
+                       "mfma_flops_issued": "SQ_INSTS_VALU_MFMA_MOPS_BF16 * 512"},
+           "cus": 256, "xcds": 8, "command": "python bench.py --collect-counters OUT"}
+    for wl, pat in PMC_WORKLOADS.items():
+        ent = {"kernel": pat or "all kernels of one forward"}
+        for tag in ("fetch", "write", "mfma"):
+            per = {}  # counter -> (sum over the workload's dispatches, dispatches)
+            calib = {}
+            disp = set()
+            for name, ctr, val, did in _rows(csv_of(wl, tag)):
+                if "neg_kernel" in name:
+                    calib[ctr] = calib.get(ctr, 0.0) + val / 3.0
+                    continue
+                if pat and pat not in name:
+                    continue
+                if not pat and ("elementwise" in name or "Fill" in name or "copy" in name.lower()):
+                    continue  # torch's own fills and copies around the block
+                t, n = per.get(ctr, (0.0, 0))
+                per[ctr] = (t + val, n)
+                disp.add(did)
+            ndisp = max(len(disp), 1)
+            launches = ndisp if pat else 2  # the decoder pass runs the block twice
+            if tag == "fetch":
+                f = calib["FETCH_SIZE"] * 1024 / COPY_BYTES
+                ent["read_bytes"] = round(per["FETCH_SIZE"][0] / launches * 1024 / f)
+                ent["fetch_factor"] = round(f, 4)
+            elif tag == "write":
+                f = calib["WRITE_SIZE"] * 1024 / COPY_BYTES
+                ent["write_bytes"] = round(per["WRITE_SIZE"][0] / launches * 1024 / f)
+                ent["write_factor"] = round(f, 4)
+            else:
+                busy = per["SQ_VALU_MFMA_BUSY_CYCLES"][0] / launches
+                gui = per["GRBM_GUI_ACTIVE"][0] / launches
+                ent["mfma_busy_simd_cycles"] = busy
+                ent["grbm_gui_active"] = gui
+                ent["sq_busy_cu_cycles"] = per["SQ_BUSY_CU_CYCLES"][0] / launches
+                ent["mfma_flops_issued"] = per["SQ_INSTS_VALU_MFMA_MOPS_BF16"][0] / launches * 512
+                ent["mfma_busy"] = round(busy / (4 * res["cus"] * gui / res["xcds"]), 4) if gui else None
+        ent["bytes"] = ent["read_bytes"] + ent["write_bytes"]
+        res[wl] = ent
+    return res
+
+
+def load_counters() -> dict:
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(COUNTERS_FILE) as f:
             return json.load(f)
     except (OSError, ValueError):
         return {}
@@ -451,19 +554,23 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--all", action="store_true", help="also the GEMM, long-context and decoder configs")
     ap.add_argument("--gemm-shapes", action="store_true", help="only the GEMM shapes beside torch.mm, one JSON line")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--report", default=None, help="write the full result dict as JSON here")
-    ap.add_argument("--pmc-pass", action="store_true", help="eager launches for a rocprofv3 --pmc run, no timing")
-    ap.add_argument("--parse-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
-                    help=f"turn two counter-collection CSVs into {os.path.relpath(TRAFFIC_FILE, ROOT)}")
+    ap.add_argument("--pmc-pass", metavar="WORKLOAD", help="eager launches of one workload for a rocprofv3 --pmc run")
+    ap.add_argument("--collect-counters", metavar="OUT",
+                    help=f"run every counter pass under rocprofv3 into OUT and write "
+                         f"{os.path.relpath(COUNTERS_FILE, ROOT)}")
+    ap.add_argument("--parse-counters", metavar="OUT", help="rewrite the counters file from an earlier OUT")
     args = ap.parse_args()
-    if args.parse_traffic:
-        t = parse_traffic(*args.parse_traffic)
-        with open(TRAFFIC_FILE, "w") as f:
-            json.dump(t, f, indent=1)
-        print(json.dumps(t))
+    if args.parse_counters:
+        out = parse_counters(os.path.abspath(args.parse_counters))
+        with open(COUNTERS_FILE, "w") as f:
+            json.dump(out, f, indent=1)
+        print(json.dumps(out))
+        return 0
+    if args.collect_counters:  # spawns the profiled runs; this process never touches the GPU
+        print(json.dumps(collect_counters(args.collect_counters)))
         return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py measures one GPU: the kernel set has no multi-GPU path (asked for {args.gpus} GPUs).",
@@ -479,7 +586,7 @@ def main() -> int:
         return 1
     _lib.lib()
     if args.pmc_pass:
-        pmc_pass()
+        pmc_pass(args.pmc_pass)
         return 0
     props = torch.cuda.get_device_properties(0)
     log(f"device: {props.name} CUs={props.multi_processor_count} lib={_lib.LIB_PATH}")
@@ -487,6 +594,7 @@ def main() -> int:
         print(json.dumps({"gemm_shapes": bench_gemm_shapes(args.steps, args.warmup)}), flush=True)
         return 0
 
+    ctr = load_counters()
     A = dict(H=8, S=2048, d=128)
     log(f"attention {A} ...")
     att, bufs = bench_attention(A["H"], A["S"], A["d"], args.steps, args.warmup)
@@ -498,8 +606,24 @@ def main() -> int:
     copy = bench_copy_ceiling(4096, 2048, args.steps, args.warmup)
     log(f"  copy     {copy['us']:.2f} us  {copy['GB/s']:.0f} GB/s  {100 * copy['frac']:.1f}% of HBM peak "
         f"(the same 32 MiB of traffic, no arithmetic)")
+    log("matmul 1024^3 bf16 ...")
+    mm = bench_matmul(args.steps, args.warmup)
+    log(f"  {mm['us']:.2f} us  {mm['tflops']:.1f} TFLOP/s")
+    long_ctx = {}
+    for H, S in ((1, 4096), (32, 16384)):
+        log(f"attention {H}x{S}x128 ...")
+        big = S > 4096
+        r, _ = bench_attention(H, S, 128, max(3, args.steps // 10) if big else args.steps, min(args.warmup, 2),
+                               sets=2 if big else None)
+        log(f"  {r['us']:.2f} us  {r['tflops']:.1f} TFLOP/s")
+        long_ctx[f"attention_{H}x{S}"] = {
+            "us": round(r["us"], 3), "tflops": round(r["tflops"], 3), "flops_per_launch": r["flops"],
+            "roofline": roofline("mfma", r["tflops"], "TFLOP/s", ctr.get(f"attention_{H}x{S}"))}
+    log("decoder block ...")
+    dec = bench_decoder(max(3, args.steps // 10), 2, ctr)
+    log(f"  split {dec['us']:.1f} us ({dec['rel_err_vs_fp32_block']:.2e} vs fp32 block); "
+        f"bf16 {dec['bf16_activations']['us']:.1f} us ({dec['bf16_activations']['rel_err_vs_fp32_block']:.2e})")
 
-    traffic = load_traffic()
     result = {
         "metric": METRIC, "value": round(att["tflops"], 3), "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(att["us"] / 1e3, 6),
@@ -509,28 +633,22 @@ def main() -> int:
                    "H": 8, "S": 2048, "d": 128,
                    "flops_per_step": att["flops"], "flop_count": "exact causal pairs 4*H*d*S(S+1)/2",
                    "device": props.name, "cus": props.multi_processor_count},
-        "roofline": roofline("mfma", att["tflops"], "TFLOP/s", traffic.get("attention", {}).get("bytes")),
+        "roofline": roofline("mfma", att["tflops"], "TFLOP/s", ctr.get("attention")),
         "row_kernels": {k: {"us": round(r["us"], 3), "GB/s": round(r["GB/s"], 1), "frac": round(r["frac"], 4),
                             "bytes": r["bytes"], "frac_of_copy_ceiling": round(r["GB/s"] / copy["GB/s"], 4),
-                            "roofline": roofline("hbm", r["GB/s"], "GB/s", traffic.get(k, {}).get("bytes"))}
+                            "roofline": roofline("hbm", r["GB/s"], "GB/s", ctr.get(k))}
                         for k, r in rows.items()},
         "hbm_copy_ceiling": {"us": round(copy["us"], 3), "GB/s": round(copy["GB/s"], 1),
                              "frac": round(copy["frac"], 4), "bytes": copy["bytes"], "copy_exact": copy["copy_exact"],
                              "kernel": "nkl_stream_copy: the row kernels' loads and non-temporal stores, no arithmetic"},
+        "matmul": {"M": 1024, "N": 1024, "K": 1024, "us": round(mm["us"], 3), "tflops": round(mm["tflops"], 3),
+                   "flops_per_launch": 2 * 1024 ** 3,
+                   "roofline": roofline("mfma", mm["tflops"], "TFLOP/s", ctr.get("matmul"))},
+        **long_ctx,
+        "decoder_block": dec,
     }
-    if args.all:
-        log("matmul 1024^3 bf16 ...")
-        result["matmul"] = bench_matmul(args.steps, args.warmup)
-        for H, S in ((1, 4096), (32, 16384)):
-            log(f"attention {H}x{S}x128 ...")
-            r, _ = bench_attention(H, S, 128, max(3, args.steps // 10 if S > 4096 else args.steps), args.warmup,
-                                   sets=2 if S > 4096 else None)
-            result[f"attention_{H}x{S}"] = {k: r[k] for k in ("us", "tflops")} | {
-                "frac": r["tflops"] / PEAK_BF16_TFLOPS}
-        log("decoder block ...")
-        result["decoder_block"] = bench_decoder(max(3, args.steps // 10), 2)
-        log("GEMM shapes (nkl_gemm and torch.mm) ...")
-        result["gemm_shapes"] = bench_gemm_shapes(max(3, args.steps // 5), 2)
+    if ctr:
+        result["counters_source"] = os.path.relpath(COUNTERS_FILE, ROOT)
     if not args.no_cpu:
         log("CPU baseline ...")
         q, k, v, o = bufs

@@ -68,3 +68,20 @@ def decoder_inputs(S=2048, d_model=2048, n_heads=16, d_ff=5632, eps=1e-6, seed=0
         block.norm2.weight.fill_(1.0)
     x = _normal(rng, (S, d_model), dtype=torch.float32)
     return block, x
+
+
+# Algorithmic work of the benchmark configurations (the roofline numerators).
+
+def causal_flops(H: int, S: int, d: int) -> int:
+    """Exact FLOPs of causal attention: 4 d per (query, key <= query) pair,
+    4 H d S (S + 1) / 2 (two products of d multiply-adds per pair)."""
+    return 4 * H * d * S * (S + 1) // 2
+
+
+def decoder_flops(S=2048, d_model=2048, n_heads=16, d_ff=5632) -> int:
+    """FLOPs of one decoder block forward: the five projections (2 M N K
+    each) and causal attention."""
+    hd = d_model // n_heads
+    gemm = 2 * S * d_model * (3 * d_model) + 2 * S * d_model * d_model + 2 * (2 * S * d_model * d_ff) + \
+        2 * S * d_ff * d_model
+    return gemm + causal_flops(n_heads, S, hd)
