@@ -261,10 +261,15 @@ void flash_fwd_kernel(AttnArgs p, Work w) {
     };
 
     floatx16 s_cur;
+    bf16x8 va[4][2];  // V^T fragments of the tile being multiplied (read one step ahead)
     if (nw > 0) {
       bf16x8 kf[8];
 #pragma unroll
       for (int f = 0; f < 8; ++f) kf[f] = kfrag(0, f);
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int uu = 0; uu < 2; ++uu) va[db][uu] = vfrag(0, db, uu);
 #pragma unroll
       for (int e = 0; e < 16; ++e) s_cur[e] = 0.f;
 #pragma unroll
@@ -287,18 +292,13 @@ void flash_fwd_kernel(AttnArgs p, Work w) {
       __builtin_amdgcn_sched_barrier(0);
       const float mneg = m_run == -INFINITY ? 0.f : -m_run;
       floatx16 s_nxt;
-      bf16x8 va[4][2];
-      // ---- region 1: S(j+1) = K(j+1) Q^T  x  exp, row sum, bf16 P(j); V^T reads of tile j
+      // ---- region 1: S(j+1) = K(j+1) Q^T  x  exp, row sum, bf16 P(j)
       if (next) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) s_nxt[e] = 0.f;
 #pragma unroll
         for (int f = 0; f < 8; ++f) s_nxt = MF::mma(kf[f], qf[f], s_nxt);
       }
-#pragma unroll
-      for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int uu = 0; uu < 2; ++uu) va[db][uu] = vfrag(st, db, uu);
       float rs = 0.f;
       bf16x8 pf[2];
 #pragma unroll
@@ -311,23 +311,27 @@ void flash_fwd_kernel(AttnArgs p, Work w) {
 #pragma unroll
         for (int f = 0; f < 8; ++f) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // two LDS reads
           __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
         }
       }
       __builtin_amdgcn_sched_barrier(0);
       l_run += rs;
-      // ---- region 2: O += P(j) V(j)  x  (mask and) row max of S(j+1)
+      // ---- region 2: O += P(j) V(j)  x  (mask and) row max of S(j+1), and
+      // the V^T fragments of tile j+1 read into the registers each MFMA frees
 #pragma unroll
       for (int db = 0; db < 4; ++db)
 #pragma unroll
-        for (int uu = 0; uu < 2; ++uu) oacc[db] = MF::mma(va[db][uu], pf[uu], oacc[db]);
+        for (int uu = 0; uu < 2; ++uu) {
+          oacc[db] = MF::mma(va[db][uu], pf[uu], oacc[db]);
+          if (next) va[db][uu] = vfrag(sn, db, uu);
+        }
       float mx = 0.f;
       if (next) {
         mx = msk ? mask_max(s_nxt) : plain_max(s_nxt);
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+          __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
           __builtin_amdgcn_sched_group_barrier(0x002, 2, 1);
         }
       }
