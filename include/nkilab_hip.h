@@ -267,6 +267,26 @@ int nkl_attention_naive_gqa(const void* q, const void* k, const void* v,
                             void* stream);
 
 /*
+ * nkl_flash_attn_causal_gqa without the scratch arguments, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * The partial states and arrival counters live in a static device array of
+ * 64 MiB + 1 MiB that each GPU holds from its first call until the process
+ * ends; a shape whose nkl_flash_attn_causal_workspace_bytes() exceeds 64 MiB
+ * (or whose counters, 4 H ceil(S / 64) bytes, exceed 1 MiB) is rejected with
+ * NKL_EWORKSPACE.  The call allocates nothing and clears the counters with a
+ * kernel (no memset node), so it may be captured; make the first call on each
+ * device outside capture (it looks the array's address up).  Every call on a
+ * GPU shares that GPU's array: calls that may overlap on one GPU (other
+ * streams, other threads) race and must be serialised by the caller.
+ */
+int nkl_flash_attn_causal_noalloc(const void* q, const void* k, const void* v,
+                                  void* o, int H, int Hkv, int S, int d,
+                                  long q_sh, long q_ss, long k_sh, long k_ss,
+                                  long v_sh, long v_ss, long o_sh, long o_ss,
+                                  float scale, int dtype, void* stream);
+
+/*
  * Rotary position embedding, rotate-half layout (RoFormer, as GPT-NeoX and
  * Llama apply it): for each head h and row s of x [H, S, d] (strides x_sh,
  * x_ss; d even), element i < d/2 and element i + d/2 rotate by the angle

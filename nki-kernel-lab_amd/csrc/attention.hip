@@ -407,6 +407,71 @@ extern "C" int nkl_flash_attn_causal_gqa(const void* q, const void* k, const voi
                      true, H, Hkv, S, d, strides, scale, dtype, stream);
 }
 
+// Scratch of the allocation-free entry point: kNoAllocPartBytes of partial
+// states, then kNoAllocCounterBytes of arrival counters.  Each GPU the library
+// runs on holds its own copy from the first call until the process ends.  In
+// host code the array's name is not a device address: kernels and fills get
+// the per-device address hipGetSymbolAddress returns.
+constexpr size_t kNoAllocPartBytes = (size_t)64 << 20;
+constexpr size_t kNoAllocCounterBytes = (size_t)1 << 20;
+constexpr int kNoAllocMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kNoAllocPartBytes + kNoAllocCounterBytes];
+static void* scratch_addr[kNoAllocMaxDevices];
+
+static __global__ void zero_words_kernel(int* p, long n) {
+  for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) p[i] = 0;
+}
+
+// The current device's copy of `scratch`, looked up once per device.  Two
+// threads racing on a device's first call both store the same address.
+static int scratch_of_current_device(const char* fn, unsigned char** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kNoAllocMaxDevices)
+    return set_error(NKL_ELAUNCH, "%s: no usable current device (%d)", fn, dev);
+  void* p = __atomic_load_n(&scratch_addr[dev], __ATOMIC_ACQUIRE);
+  if (!p) {
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(NKL_ELAUNCH, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", fn, dev,
+                       hipGetErrorString(e));
+    __atomic_store_n(&scratch_addr[dev], p, __ATOMIC_RELEASE);
+  }
+  *out = static_cast<unsigned char*>(p);
+  return NKL_OK;
+}
+
+extern "C" int nkl_flash_attn_causal_noalloc(const void* q, const void* k, const void* v, void* o, int H, int Hkv,
+                                             int S, int d, long q_sh, long q_ss, long k_sh, long k_ss, long v_sh,
+                                             long v_ss, long o_sh, long o_ss, float scale, int dtype, void* stream) {
+  const char* fn = "nkl_flash_attn_causal_noalloc";
+  const long strides[8] = {q_sh, q_ss, k_sh, k_ss, v_sh, v_ss, o_sh, o_ss};
+  int rc = check_attn(fn, q, k, v, o, H, S, d, dtype, strides);
+  if (rc) return rc;
+  if (dtype != NKL_BF16 || H == 0 || S == 0)  // no scratch on these paths
+    return flash_entry(fn, q, k, v, o, nullptr, 0, nullptr, 0, true, H, Hkv, S, d, strides, scale, dtype, stream);
+  const size_t need = flash_bf16_workspace_bytes(H, S, d);
+  // One counter per 64-query block (the smallest block) covers every schedule.
+  const size_t need_c = need ? (size_t)H * ((S + 63) / 64) * 4 : 0;
+  if (need > kNoAllocPartBytes || need_c > kNoAllocCounterBytes)
+    return set_error(NKL_EWORKSPACE,
+                     "%s: H=%d S=%d d=%d needs %zu bytes of partial states and %zu of counters; the static scratch "
+                     "holds %zu and %zu (use nkl_flash_attn_causal_gqa with a workspace)",
+                     fn, H, S, d, need, need_c, kNoAllocPartBytes, kNoAllocCounterBytes);
+  unsigned char* base = nullptr;
+  if ((rc = scratch_of_current_device(fn, &base))) return rc;
+  int* counters = reinterpret_cast<int*>(base + kNoAllocPartBytes);
+  if (need_c > 0) {
+    // The kernels leave the counters zero; clear them anyway, with a kernel
+    // (not a memset node) so that the call can be captured in a graph.
+    const long n = (long)(need_c / 4);
+    zero_words_kernel<<<dim3((unsigned)((n + 255) / 256 < 64 ? (n + 255) / 256 : 64)), dim3(256), 0,
+                        (hipStream_t)stream>>>(counters, n);
+    if ((rc = check_launch(fn))) return rc;
+  }
+  return flash_entry(fn, q, k, v, o, need ? base : nullptr, need, counters, need_c, true, H, Hkv, S, d, strides,
+                     scale, dtype, stream);
+}
+
 extern "C" int nkl_flash_attn_configure(int kernel, int schedule, int qb, int cpb) {
   return flash_bf16_configure(kernel, schedule, qb, cpb);
 }

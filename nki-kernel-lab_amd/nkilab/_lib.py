@@ -45,6 +45,9 @@ SIGNATURES = {
     "nkl_flash_attn_causal_gqa": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_size, _vp, _c_size, _c_int, _c_int, _c_int,
                                            _c_int, _c_long, _c_long, _c_long, _c_long, _c_long, _c_long, _c_long,
                                            _c_long, _c_float, _c_int, _vp]),
+    "nkl_flash_attn_causal_noalloc": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_long,
+                                               _c_long, _c_long, _c_long, _c_long, _c_long, _c_long, _c_long,
+                                               _c_float, _c_int, _vp]),
     "nkl_attention_naive_gqa": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_size, _c_int, _c_int, _c_int, _c_int, _c_long,
                                          _c_long, _c_long, _c_long, _c_long, _c_long, _c_long, _c_long, _c_float,
                                          _c_int, _vp]),

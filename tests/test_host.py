@@ -105,6 +105,26 @@ def test_gemm_swiglu_abi_checks():
     assert L.nkl_gemm_swiglu(None, None, None, 0, 64, 64, 64, 64, 64, 1, None) == 0   # empty
 
 
+def test_noalloc_attention_rejects_shapes_beyond_its_static_scratch():
+    """The allocation-free entry holds 1 MiB of arrival counters (one per
+    64-query block): a balanced launch over 2^24 + 64 positions needs one more
+    and is refused before any device memory is touched."""
+    from nkilab import _lib
+
+    L = _lib.lib()
+    _lib.flash_configure(kernel="teams", schedule="balanced")
+    try:
+        S = (1 << 24) + 64
+        rc = L.nkl_flash_attn_causal_noalloc(None, None, None, None, 1, 1, S, 128, 0, 128, 0, 128, 0, 128, 0, 128,
+                                             ctypes.c_float(0.1), 1, None)
+        assert rc == -4, L.nkl_last_error_string()
+        assert b"static scratch" in L.nkl_last_error_string()
+    finally:
+        _lib.flash_configure()
+    assert L.nkl_flash_attn_causal_noalloc(None, None, None, None, 1, 1, 16, 256, 0, 0, 0, 0, 0, 0, 0, 0,
+                                           ctypes.c_float(0.1), 1, None) == -1  # d > 128
+
+
 def test_rope_and_gqa_abi_checks():
     from nkilab import _lib
 
