@@ -449,6 +449,19 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
         const float4* xo = reinterpret_cast<const float4*>(smem) + (t2 * WPT + wq) * (L::SLOT / 4) + lane;
         fold_state([&](int k) __attribute__((always_inline)) { return xo[k * 64]; });
       }
+    if constexpr (NT > 1) {
+      // l summed over the teams in team order from their (m, l) in LDS, the
+      // same sum in every team (the folds above add in a team-dependent
+      // order): the merge of a split block, which starts either from a team's
+      // registers or from the (m, l) team 0 stored, then gives the same bits.
+      float lc = 0.f;
+#pragma unroll
+      for (int t2 = 0; t2 < NT; ++t2) {
+        const float4 st = (reinterpret_cast<const float4*>(smem) + (t2 * WPT + wq) * (L::SLOT / 4) + lane)[L::NCO * 64];
+        lc += st.x == -INFINITY ? 0.f : st.y * fast_exp2(st.x - m_run);
+      }
+      l_tot = lc;
+    }
 
     // Writes this team's d-blocks of O / l for the wavefront's 32 queries.
     // The lane layout of O^T (lane: one query, 4-column groups of d) would
@@ -529,9 +542,23 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
       if (arrival == nparts - 1) {  // last to arrive: merge the others and write O
         // The others' states were complete before their arrivals, which
         // precede this one; device-coherent loads read them from memory.
+        // The parts are folded last range first, whichever workgroup arrived
+        // last, so the result is bitwise reproducible: the holder of the last
+        // range (the usual last arriver) starts from its own registers; any
+        // other restarts from an empty state and reads its own part back (a
+        // fold into an empty state copies a part exactly).
+        const int vl = vf + nparts - 1;
+        if (vidx != vl) {
+          m_run = -INFINITY;
+          l_tot = 0.f;
+#pragma unroll
+          for (int j = 0; j < OWN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) own[j][e] = 0.f;
+        }
 #pragma unroll 1
-        for (int v2 = vf; v2 < vf + nparts; ++v2) {
-          if (v2 == vidx) continue;
+        for (int v2 = vl; v2 >= vf; --v2) {
+          if (v2 == vidx && vidx == vl) continue;
           const int slot2 = range_start(v2, w) >= bstart ? 0 : 1;
           fold_state([&](int k) __attribute__((always_inline)) {
             return __builtin_bit_cast(float4,
@@ -1065,9 +1092,23 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
       if (more) load_q(nxt);
       __syncthreads();
       if (arrival == nparts - 1) {
+        // Folded last range first, whichever workgroup arrived last (the
+        // order of the teams kernel above): bitwise reproducible.
+        const int vl = vf + nparts - 1;
+        if (vidx != vl) {
+#pragma unroll
+          for (int hq = 0; hq < QH; ++hq) {
+            m_run[hq] = -INFINITY;
+            l_tot[hq] = 0.f;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+              for (int e = 0; e < 16; ++e) oacc[hq][db][e] = 0.f;
+          }
+        }
 #pragma unroll 1
-        for (int v2 = vf; v2 < vf + nparts; ++v2) {
-          if (v2 == vidx) continue;
+        for (int v2 = vl; v2 >= vf; --v2) {
+          if (v2 == vidx && vidx == vl) continue;
           const int slot2 = range_start(v2, w) >= bstart ? 0 : 1;
 #pragma unroll
           for (int hq = 0; hq < QH; ++hq) {

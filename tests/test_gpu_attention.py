@@ -14,6 +14,13 @@ pytestmark = pytest.mark.gpu
 
 VARIANTS = ["naive", "flash", "flash_kv_resident", "flash_balanced", "flash_pipelined"]
 
+# bf16 outputs on random N(0, 1) inputs, against fp32 SDPA or the oracle: the
+# reference's own algorithm in bf16 arithmetic (the oracle) is up to 3.1e-3
+# from fp32 SDPA on such inputs (30 seeded cases of the shapes below), from the
+# bf16 rounding of P and of O itself (2^-9 of an element).  The benchmark
+# configurations are held to 3e-3.
+BF16_TOL = 4e-3
+
 
 def _bf(t):
     return torch.from_numpy(np.asarray(t, np.float32)).to(torch.bfloat16).cuda()
@@ -49,7 +56,7 @@ def test_attention_bf16(rng, variant):
     ref = _sdpa_cpu(*(_np(t) for t in (q, k, v)))
     out = ops.attention(q, k, v, variant=variant)
     assert out.dtype == torch.bfloat16
-    assert rel_err(_np(out), ref) < 3e-2
+    assert rel_err(_np(out), ref) <= BF16_TOL
 
 
 def test_first_token_attends_only_to_itself(rng):
@@ -83,7 +90,7 @@ def test_attention_matches_golden_vectors():
             else:
                 # P is rounded to bf16 relative to a running max that depends on the
                 # key tiling, so bf16 results agree to the bf16 tolerance, not bitwise.
-                assert rel_err(out, ref) < 1e-2, (tag, var)
+                assert rel_err(out, ref) <= BF16_TOL, (tag, var)
 
 
 def test_strided_heads_layout(rng):
@@ -99,7 +106,7 @@ def test_strided_heads_layout(rng):
     ops.attention_into(q, k, v, merged.view(S, H, hd).transpose(0, 1))
     ref = _sdpa_cpu(*(_np(t.contiguous()) for t in (q, k, v)))  # [H, S, hd]
     got = _np(merged).reshape(S, H, hd).transpose(1, 0, 2)
-    assert rel_err(got, ref) < 1e-2
+    assert rel_err(got, ref) <= BF16_TOL
 
 
 def test_flash_scratch_reused_across_shapes(rng):
@@ -111,7 +118,7 @@ def test_flash_scratch_reused_across_shapes(rng):
         q, k, v = (_bf(rng.standard_normal((H, S, d))) for _ in range(3))
         out = _np(ops.attention(q, k, v))
         ref = _sdpa_cpu(*(_np(t) for t in (q, k, v)))
-        assert rel_err(out, ref) < 1e-2, (H, S, d)
+        assert rel_err(out, ref) <= BF16_TOL, (H, S, d)
 
 
 SCHEDULES = [(qb, s) for qb in ("64", "128") for s in ("balanced", "pairs", "block")]
@@ -132,8 +139,8 @@ def test_flash_bf16_schedules(rng, flash_cfg, kernel, qb, schedule, H, S, d):
     q, k, v = (_bf(rng.standard_normal((H, S, d))) for _ in range(3))
     out = _np(ops.attention(q, k, v))
     ref = _sdpa_cpu(*(_np(t) for t in (q, k, v)))
-    assert rel_err(out, ref) < 1e-2, (schedule, H, S, d)
-    np.testing.assert_allclose(out[:, 0], _np(v)[:, 0], atol=1e-2)  # query 0 sees only key 0
+    assert rel_err(out, ref) <= BF16_TOL, (schedule, H, S, d)
+    np.testing.assert_allclose(out[:, 0], _np(v)[:, 0], rtol=2 ** -8, atol=0)  # query 0 sees only key 0
 
 
 @pytest.mark.parametrize("kernel", ["w1", "w1o2", "w64", "w64x4", "fwd"])
@@ -149,8 +156,8 @@ def test_flash_bf16_one_wave_per_simd_kernel(rng, flash_cfg, kernel, schedule, H
     q, k, v = (_bf(rng.standard_normal((H, S, d))) for _ in range(3))
     out = _np(ops.attention(q, k, v))
     ref = _sdpa_cpu(*(_np(t) for t in (q, k, v)))
-    assert rel_err(out, ref) < 1e-2, (kernel, schedule, H, S, d)
-    np.testing.assert_allclose(out[:, 0], _np(v)[:, 0], atol=1e-2)
+    assert rel_err(out, ref) <= BF16_TOL, (kernel, schedule, H, S, d)
+    np.testing.assert_allclose(out[:, 0], _np(v)[:, 0], rtol=2 ** -8, atol=0)
 
 
 @pytest.mark.parametrize("kernel", ["w1", "w1o2", "w64", "w64x4", "teams4", "fwd"])
@@ -184,17 +191,31 @@ def test_flash_bf16_balanced_block_start_cost(rng, flash_cfg, kernel, qb, cpb, H
     """The balanced split with block start costs from none to more than a
     range holds (the planner lowers it until every range keeps a unit): every
     unit is computed once and every split block merged once, whatever the
-    ranges; two calls in a row agree within the merge-order rounding."""
+    ranges; two calls in a row agree bitwise (the parts of a split block are
+    folded in a fixed order, whichever workgroup arrives last)."""
     from nkilab import ops
 
     flash_cfg(kernel=kernel, schedule="balanced", qb=qb, cpb=cpb)
     q, k, v = (_bf(rng.standard_normal((H, S, d))) for _ in range(3))
     out = _np(ops.attention(q, k, v))
     ref = _sdpa_cpu(*(_np(t) for t in (q, k, v)))
-    assert rel_err(out, ref) < 1e-2, (kernel, qb, cpb, H, S, d)
-    np.testing.assert_allclose(out[:, 0], _np(v)[:, 0], atol=1e-2)
-    again = _np(ops.attention(q, k, v))
-    assert np.abs(again - out).max() <= 2 ** -6 * max(1.0, float(np.abs(out).max()))
+    assert rel_err(out, ref) <= BF16_TOL, (kernel, qb, cpb, H, S, d)
+    np.testing.assert_allclose(out[:, 0], _np(v)[:, 0], rtol=2 ** -8, atol=0)
+    for _ in range(3):
+        np.testing.assert_array_equal(_np(ops.attention(q, k, v)), out)
+
+
+@pytest.mark.parametrize("H,S", [(8, 2048), (1, 4096), (8, 8192), (3, 1537)])
+def test_default_attention_is_bitwise_reproducible(H, S):
+    """The automatic choice (teams kernel over balanced ranges with 64- or
+    128-query blocks, or the two-wavefront-per-SIMD kernel over balanced
+    ranges at 8 x 8192): repeated calls give identical bits."""
+    from nkilab import ops, workloads
+
+    q, k, v = (t.cuda() for t in workloads.attention_inputs(H, S, 128))
+    first = ops.attention(q, k, v)
+    for _ in range(4):
+        assert torch.equal(ops.attention(q, k, v), first), (H, S)
 
 
 # ------------------------------------------------ benchmark configurations --
@@ -277,8 +298,8 @@ def test_gqa_attention_matches_sdpa_on_repeated_kv(rng, variant, H, Hkv, S, d):
     qb, kb, vb = (_bf(t) for t in (q, k, v))
     outb = _np(ops.attention(qb, kb, vb, variant=variant))
     refb = _sdpa_cpu(_np(qb), rep(_np(kb)), rep(_np(vb)))
-    assert rel_err(outb, refb) < 1e-2, ("bf16", variant)
-    assert rel_err(outb, O.ops_attention(_np(qb), _np(kb), _np(vb), variant, O.BF16)) < 1e-2
+    assert rel_err(outb, refb) <= BF16_TOL, ("bf16", variant)
+    assert rel_err(outb, O.ops_attention(_np(qb), _np(kb), _np(vb), variant, O.BF16)) <= BF16_TOL
 
 
 @pytest.mark.parametrize("kernel,qb,schedule", [("teams", "128", "balanced"), ("teams", "64", "balanced"),
@@ -294,4 +315,4 @@ def test_gqa_bf16_every_kernel_and_schedule(rng, flash_cfg, kernel, qb, schedule
     k, v = (_bf(rng.standard_normal((Hkv, S, d))) for _ in range(2))
     out = _np(ops.attention(q, k, v))
     ref = _sdpa_cpu(_np(q), *(np.repeat(_np(t), H // Hkv, axis=0) for t in (k, v)))
-    assert rel_err(out, ref) < 1e-2, (kernel, qb, schedule)
+    assert rel_err(out, ref) <= BF16_TOL, (kernel, qb, schedule)
