@@ -55,6 +55,7 @@ constexpr int BN = 32;  // keys per tile
 // half the CUs idle at 2 x 2048: 24.7 -> 20.6 us at 8; 2 x 1024: 25.5 -> 17.6).
 constexpr long kMinUnits = 8;
 
+
 template <int D, int WPT, int NT>
 struct Layout {
   static constexpr int QB = 32 * WPT;      // queries per block
@@ -525,20 +526,27 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), prsrc, poff(vidx, slot, k), 0,
                                                kDeviceCoherent);
       };
-      if (keeps) {
+      // The holder of the block's last range waits for the other parts to
+      // arrive instead of storing its own state (see await_parts).
+      const int vl = vf + nparts - 1;
+      if (vidx == vl) await_parts(&w.count[hh * w.nqb + b], nparts, arrival);
+      if (vidx != vl || arrival != nparts - 1) {
+        if (keeps) {
 #pragma unroll
-        for (int j = 0; j < OWN; ++j)
+          for (int j = 0; j < OWN; ++j)
 #pragma unroll
-          for (int k = 0; k < 4; ++k)
-            pstore(4 * (own0 + j) + k, make_float4(own[j][4 * k], own[j][4 * k + 1], own[j][4 * k + 2], own[j][4 * k + 3]));
+            for (int k = 0; k < 4; ++k)
+              pstore(4 * (own0 + j) + k,
+                     make_float4(own[j][4 * k], own[j][4 * k + 1], own[j][4 * k + 2], own[j][4 * k + 3]));
+        }
+        if (team == 0) pstore(L::NCO, make_float4(m_run, l_tot, 0.f, 0.f));
+        // Release: every wavefront's device-coherent stores have completed
+        // (vmcnt) before the barrier and so before the arrival atomic.
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) arrival = atomicAdd(&w.count[hh * w.nqb + b], 1);
+        __syncthreads();
       }
-      if (team == 0) pstore(L::NCO, make_float4(m_run, l_tot, 0.f, 0.f));
-      // Release: every wavefront's device-coherent stores have completed
-      // (vmcnt) before the barrier and so before the arrival atomic.
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-      if (tid == 0) arrival = atomicAdd(&w.count[hh * w.nqb + b], 1);
-      __syncthreads();
       if (arrival == nparts - 1) {  // last to arrive: merge the others and write O
         // The others' states were complete before their arrivals, which
         // precede this one; device-coherent loads read them from memory.
@@ -547,7 +555,6 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
         // range (the usual last arriver) starts from its own registers; any
         // other restarts from an empty state and reads its own part back (a
         // fold into an empty state copies a part exactly).
-        const int vl = vf + nparts - 1;
         if (vidx != vl) {
           m_run = -INFINITY;
           l_tot = 0.f;
@@ -1072,8 +1079,11 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
         return 4 * (((v * 2 + s2) * PART) + wq * SLOT + hq * HS + k * 256 + 4 * lane);
       };
       const int slot = range_start(vidx, w) >= bstart ? 0 : 1;
+      const int vl = vf + nparts - 1;
+      if (vidx == vl) await_parts(&w.count[hh * w.nqb + b], nparts, arrival);
+      const bool stored = vidx != vl || arrival != nparts - 1;
 #pragma unroll
-      for (int hq = 0; hq < QH; ++hq) {
+      for (int hq = 0; hq < QH && stored; ++hq) {
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -1086,15 +1096,16 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
             __builtin_bit_cast(u32x4, make_float4(m_run[hq], l_tot[hq], 0.f, 0.f)), prsrc,
             poff(vidx, slot, hq, NCO), 0, kDeviceCoherent);
       }
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-      if (tid == 0) arrival = atomicAdd(&w.count[hh * w.nqb + b], 1);
+      if (stored) {
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) arrival = atomicAdd(&w.count[hh * w.nqb + b], 1);
+      }
       if (more) load_q(nxt);
       __syncthreads();
       if (arrival == nparts - 1) {
         // Folded last range first, whichever workgroup arrived last (the
         // order of the teams kernel above): bitwise reproducible.
-        const int vl = vf + nparts - 1;
         if (vidx != vl) {
 #pragma unroll
           for (int hq = 0; hq < QH; ++hq) {

@@ -507,7 +507,11 @@ void flash_fwd_kernel(AttnArgs p, Work w) {
         const int s = range_start(v, w) >= bstart ? 0 : 1;
         return ((v * 2 + s) * 8 + wid) * (PCH * 1024) + lane * 16;
       };
-      {
+      // The holder of the block's last range merges: it waits for the other
+      // parts' arrivals instead of storing its own state (await_parts).
+      const int vl = vf + nparts - 1;
+      if (vidx == vl) await_parts(&w.count[hh * w.nqb + b], nparts, arrival);
+      if (vidx != vl || arrival != nparts - 1) {
         const int base = pbase(vidx);
 #pragma unroll
         for (int t = 0; t < 2; ++t)
@@ -519,13 +523,13 @@ void flash_fwd_kernel(AttnArgs p, Work w) {
                 prsrc, base + (4 * t + k) * 1024, 0, kDeviceCoherent);
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, make_float4(m_run, l_tot, 0.f, 0.f)), prsrc,
                                                base + 8 * 1024, 0, kDeviceCoherent);
+        // Release: every wavefront's device-coherent stores have completed
+        // before the barrier and so before the arrival atomic.
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) arrival = atomicAdd(&w.count[hh * w.nqb + b], 1);
+        __syncthreads();
       }
-      // Release: every wavefront's device-coherent stores have completed
-      // before the barrier and so before the arrival atomic.
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-      if (tid == 0) arrival = atomicAdd(&w.count[hh * w.nqb + b], 1);
-      __syncthreads();
       if (arrival == nparts - 1) {
         // Last to arrive: the others' states were complete before their
         // arrivals, which precede this one; device-coherent loads read them.

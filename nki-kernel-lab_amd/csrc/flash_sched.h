@@ -190,6 +190,27 @@ __device__ __forceinline__ Seg decode_seg(long u, long u0, const Work& w) {
   return sg;
 }
 
+// The workgroup holding a split block's last range merges it.  It walks that
+// segment last, long after the block's other parts -- walked first by their
+// ranges -- have stored their states and arrived, so rather than store its own
+// state and arrive it polls the block's counter until the other nparts - 1
+// have arrived (their arrivals never reach nparts - 1 without it) and sets
+// `arrival` to nparts - 1.  The poll is bounded (4096 polls, each followed by
+// ~512 cycles of sleep: ~1 ms); past that `arrival` is -1 and the workgroup
+// stores its state and arrives like the others, the last of which merges.
+__device__ __forceinline__ void await_parts(int* count, int nparts, int& arrival) {
+  if (threadIdx.x == 0) {
+    int n = 0;
+    for (int it = 0; it < 4096; ++it) {
+      n = __hip_atomic_load(count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (n == nparts - 1) break;
+      __builtin_amdgcn_s_sleep(8);
+    }
+    arrival = n == nparts - 1 ? nparts - 1 : -1;
+  }
+  __syncthreads();
+}
+
 // s_waitcnt with vmcnt <= n and the other counters left alone (gfx9 encoding).
 template <int n>
 __device__ __forceinline__ void wait_vm() {
