@@ -163,6 +163,43 @@ def bench_copy_ceiling(R, D, reps, warmup):
             "bytes": 2 * nb, "buffer_sets": sets, "copy_exact": ok}
 
 
+def bench_copy_curve(reps, warmup):
+    """nkl_stream_copy at 32, 48, 64, 128 and 256 MiB of traffic (half read,
+    half written), and a 16-byte copy (one workgroup: the launch alone), in
+    the same graph harness and buffer rotation as the row kernels.  A least
+    squares line through the five sizes splits a launch into a fixed cost and
+    a steady bandwidth."""
+    import torch
+
+    from nkilab import _lib
+    from nkilab._tensors import stream_handle
+
+    def one(nb):
+        sets = min(n_sets(2 * nb), 32)
+        bufs = [(torch.empty(nb // 2, dtype=torch.bfloat16, device="cuda").normal_(),
+                 torch.empty(nb // 2, dtype=torch.bfloat16, device="cuda")) for _ in range(sets)]
+        sec = time_launches([lambda b=b: _lib.call("nkl_stream_copy", b[0].data_ptr(), b[1].data_ptr(), nb,
+                                                    stream_handle()) for b in bufs], reps, warmup)
+        del bufs
+        return sec * 1e6
+
+    points = []
+    for mib in (32, 48, 64, 128, 256):
+        traffic = mib << 20
+        us = one(traffic // 2)
+        points.append({"traffic_MiB": mib, "us": round(us, 3), "GB/s": round(traffic / us / 1e3, 1),
+                       "frac": round(traffic / us / 1e3 / PEAK_HBM_GBS, 4)})
+    empty_us = one(16)
+    xs = [p["traffic_MiB"] * (1 << 20) for p in points]
+    ys = [p["us"] for p in points]
+    n = len(xs)
+    mx, my = sum(xs) / n, sum(ys) / n
+    slope = sum((x - mx) * (y - my) for x, y in zip(xs, ys)) / sum((x - mx) ** 2 for x in xs)
+    return {"points": points, "empty_launch_us": round(empty_us, 3),
+            "fit": {"fixed_us": round(my - slope * mx, 3), "steady_GB/s": round(1e-3 / slope, 1)},
+            "kernel": "nkl_stream_copy (2 x 16-byte loads per lane, non-temporal stores)"}
+
+
 def bench_matmul(reps, warmup):
     import torch
 
@@ -606,6 +643,10 @@ def main() -> int:
     copy = bench_copy_ceiling(4096, 2048, args.steps, args.warmup)
     log(f"  copy     {copy['us']:.2f} us  {copy['GB/s']:.0f} GB/s  {100 * copy['frac']:.1f}% of HBM peak "
         f"(the same 32 MiB of traffic, no arithmetic)")
+    curve = bench_copy_curve(args.steps, args.warmup)
+    pts = ", ".join(f"{c['traffic_MiB']} MiB {c['us']:.2f} us ({100 * c['frac']:.1f}%)" for c in curve["points"])
+    log(f"  copy curve: {pts}; empty launch {curve['empty_launch_us']:.2f} us; "
+        f"fit {curve['fit']['fixed_us']:.2f} us + bytes / {curve['fit']['steady_GB/s']:.0f} GB/s")
     log("matmul 1024^3 bf16 ...")
     mm = bench_matmul(args.steps, args.warmup)
     log(f"  {mm['us']:.2f} us  {mm['tflops']:.1f} TFLOP/s")
@@ -641,6 +682,7 @@ def main() -> int:
         "hbm_copy_ceiling": {"us": round(copy["us"], 3), "GB/s": round(copy["GB/s"], 1),
                              "frac": round(copy["frac"], 4), "bytes": copy["bytes"], "copy_exact": copy["copy_exact"],
                              "kernel": "nkl_stream_copy: the row kernels' loads and non-temporal stores, no arithmetic"},
+        "hbm_copy_curve": curve,
         "matmul": {"M": 1024, "N": 1024, "K": 1024, "us": round(mm["us"], 3), "tflops": round(mm["tflops"], 3),
                    "flops_per_launch": 2 * 1024 ** 3,
                    "roofline": roofline("mfma", mm["tflops"], "TFLOP/s", ctr.get("matmul"))},

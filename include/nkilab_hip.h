@@ -161,9 +161,10 @@ int nkl_split_bf16(const void* x, void* y, int rows, int cols, long ldx,
                    long ldy, void* stream);
 
 /*
- * y = x over nbytes (a multiple of 16; both pointers 16-byte aligned): the
- * row kernels' access pattern (4 16-byte chunks in flight per lane, then
- * non-temporal stores) with none of their arithmetic.  No counterpart in the
+ * y = x over nbytes (a multiple of 16; both pointers 16-byte aligned): 16-byte
+ * loads (2 in flight per lane, the fastest count on MI355X) and non-temporal
+ * stores, the row kernels' loads and stores with none of their arithmetic.
+ * A 16-byte call launches one workgroup: the launch cost alone.  No counterpart in the
  * reference: a measurement entry point that gives the HBM ceiling the row
  * kernels' roofline is read against, at their size and in the same run.
  */

@@ -322,6 +322,10 @@ static int rmsnorm_launch(const void* x, const void* w, void* y, int rows, int c
 template <typename T>
 static int swiglu_launch(const void* g, const void* u, void* y, long n, hipStream_t st) {
   constexpr int E = VecE<T>::value;
+  // Two vectors of each input per thread.  In bench.py's harness at 4096 x
+  // 2048 bf16 one per thread was no faster (10.8 against 10.7 us), four
+  // slower, and per-workgroup contiguous chunks (with or without an
+  // XCD-aware order) slower still.
   constexpr int UNROLL = 2;
   const T* gp = static_cast<const T*>(g);
   const T* up = static_cast<const T*>(u);
@@ -343,21 +347,24 @@ static int swiglu_launch(const void* g, const void* u, void* y, long n, hipStrea
   return check_launch("nkl_swiglu");
 }
 
-// Streaming copy with the row kernels' access pattern and none of their
-// arithmetic: each lane reads 4 16-byte chunks one grid span apart, then
-// writes them with non-temporal stores.  It measures the HBM ceiling the row
-// kernels' roofline is read against at the same size.
+// Streaming copy with the row kernels' loads and non-temporal stores and none
+// of their arithmetic: each lane reads kCopyUnroll 16-byte chunks one grid
+// span apart, then writes them.  Two per lane is the fastest of 1, 2, 4 and 8
+// (and of per-workgroup contiguous chunks) at 16 - 128 MiB on MI355X.  It
+// measures the HBM ceiling the row kernels' roofline is read against at the
+// same size.
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kCopyUnroll = 2;
 __global__ __launch_bounds__(256) void stream_copy_kernel(const u32x4* __restrict__ x, u32x4* __restrict__ y, long n) {
   const long base = (long)blockIdx.x * 256 + threadIdx.x, span = (long)gridDim.x * 256;
-  u32x4 v[4];
+  u32x4 v[kCopyUnroll];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
+  for (int k = 0; k < kCopyUnroll; ++k) {
     const long i = base + k * span;
     v[k] = i < n ? x[i] : u32x4{0u, 0u, 0u, 0u};
   }
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
+  for (int k = 0; k < kCopyUnroll; ++k) {
     const long i = base + k * span;
     if (i < n) __builtin_nontemporal_store(v[k], y + i);
   }
@@ -487,7 +494,7 @@ extern "C" int nkl_stream_copy(const void* x, void* y, long nbytes, void* stream
   if (!x || !y || ((uintptr_t)x & 15u) || ((uintptr_t)y & 15u))
     return set_error(NKL_EINVAL, "nkl_stream_copy: null or non-16-byte-aligned pointer");
   const long n = nbytes / 16;
-  const long grid = (n + 4 * 256 - 1) / (4 * 256);
+  const long grid = (n + kCopyUnroll * 256 - 1) / (kCopyUnroll * 256);
   if (grid > 0x7fffffffL) return set_error(NKL_EINVAL, "nkl_stream_copy: %ld bytes is too large", nbytes);
   stream_copy_kernel<<<dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream>>>(static_cast<const u32x4*>(x),
                                                                                    static_cast<u32x4*>(y), n);
