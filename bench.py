@@ -114,6 +114,61 @@ def bench_attention(H, S, d, reps, warmup, seed=0, sets=None):
             "bytes": per_set, "buffer_sets": sets}, bufs[0]
 
 
+def bench_attention_beside_sdpa(reps, warmup):
+    """This library's causal attention and torch's scaled_dot_product_attention
+    (is_causal, the ROCm flash backend) on the same inputs, same harness and
+    buffer rotation, at the benchmark shapes."""
+    import torch
+    import torch.nn.functional as F
+
+    from nkilab import ops, workloads
+
+    out = []
+    for H, S in ((8, 2048), (1, 4096), (8, 8192), (32, 16384)):
+        q, k, v = (t.cuda() for t in workloads.attention_inputs(H, S, 128))
+        big = S > 8192
+        sets = 2 if big else min(n_sets(4 * H * S * 128 * 2), 16)
+        bufs = [(q, k, v, torch.empty_like(q))] + [
+            (q.clone(), k.clone(), v.clone(), torch.empty_like(q)) for _ in range(sets - 1)]
+        r = max(3, reps // 10) if big else reps
+        ours = time_launches([lambda b=b: ops.attention_into(*b) for b in bufs], r, warmup)
+        sb = [tuple(t.unsqueeze(0) for t in b[:3]) for b in bufs]
+        with torch.nn.attention.sdpa_kernel([torch.nn.attention.SDPBackend.FLASH_ATTENTION]):
+            ref = F.scaled_dot_product_attention(*sb[0], is_causal=True)[0]
+            theirs = time_launches([lambda b=b: F.scaled_dot_product_attention(*b, is_causal=True) for b in sb], r,
+                                   warmup)
+        mine = ops.attention_into(q, k, v, torch.empty_like(q))
+        torch.cuda.synchronize()
+        flops = workloads.causal_flops(H, S, 128)
+        out.append({"H": H, "S": S, "nkilab_us": round(ours * 1e6, 2), "nkilab_tflops": round(flops / ours / 1e12, 1),
+                    "sdpa_us": round(theirs * 1e6, 2), "sdpa_tflops": round(flops / theirs / 1e12, 1),
+                    "max_abs_diff_rel": float((mine.float() - ref.float()).abs().max() / ref.float().abs().max())})
+        log(f"  {H}x{S}: nkilab {out[-1]['nkilab_us']} us, torch SDPA {out[-1]['sdpa_us']} us")
+        del bufs, sb
+    return out
+
+
+def bench_attention_sweep(reps, warmup):
+    """Time per launch of the default configuration from tiny shapes up to the
+    headline one (d = 128): how much of a launch does not scale with the work."""
+    import torch
+
+    from nkilab import ops, workloads
+
+    out = []
+    for H, S in ((1, 256), (1, 1024), (1, 2048), (8, 512), (8, 1024), (2, 2048), (4, 2048), (8, 2048), (16, 2048),
+                 (8, 4096)):
+        q, k, v = (t.cuda() for t in workloads.attention_inputs(H, S, 128))
+        sets = min(n_sets(4 * H * S * 128 * 2), 16)
+        bufs = [(q.clone(), k.clone(), v.clone(), torch.empty_like(q)) for _ in range(sets)]
+        sec = time_launches([lambda b=b: ops.attention_into(*b) for b in bufs], reps, warmup)
+        flops = workloads.causal_flops(H, S, 128)
+        out.append({"H": H, "S": S, "us": round(sec * 1e6, 2), "tflops": round(flops / sec / 1e12, 1)})
+        log(f"  {H}x{S}: {out[-1]['us']} us")
+        del bufs
+    return out
+
+
 def bench_rows(R, D, reps, warmup, seed=0):
     import torch
 
@@ -440,7 +495,11 @@ COUNTER_SETS = {"fetch": ["FETCH_SIZE"], "write": ["WRITE_SIZE"],
 # of the workload but the calibration copy)
 PMC_WORKLOADS = {"attention": "flash", "attention_1x4096": "flash", "attention_32x16384": "flash",
                  "matmul": "gemm", "softmax": "softmax_vec", "rmsnorm": "rmsnorm_vec", "swiglu": "swiglu_vec",
-                 "decoder": ""}
+                 "decoder": "", "gemm_qkv": "gemm", "gemm_wo": "gemm", "gemm_gate_up": "gemm", "gemm_down": "gemm"}
+# The decoder block's four projections at hidden 2048, FFN 5632, 2048 tokens:
+# (M, N, K); gate/up is the fused GEMM with the SwiGLU epilogue (N = 2 x 5632).
+DECODER_GEMMS = {"gemm_qkv": (2048, 6144, 2048), "gemm_wo": (2048, 2048, 2048), "gemm_gate_up": (2048, 11264, 2048),
+                 "gemm_down": (2048, 2048, 5632)}
 PMC_REPS = 8
 
 
@@ -478,6 +537,23 @@ def pmc_pass(workload: str) -> None:
                 ops.rmsnorm_into(x.clone(), w, torch.empty_like(x), 1e-6)
             else:
                 ops.swiglu_into(gate.clone(), up.clone(), torch.empty_like(gate))
+    elif workload in DECODER_GEMMS:
+        M, N, K = DECODER_GEMMS[workload]
+        g = torch.Generator().manual_seed(0)
+        a = (torch.randn(M, K, generator=g) * 1.0).to(torch.bfloat16).cuda()
+        sets = []
+        for _ in range(4):
+            w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).cuda()
+            if workload == "gemm_gate_up":
+                w = ops.pack_gate_up(w[: N // 2], w[N // 2:])
+                sets.append((a, w, torch.empty(M, N // 2, dtype=torch.bfloat16, device="cuda")))
+            else:
+                sets.append((a, w, torch.empty(M, N, dtype=torch.bfloat16, device="cuda")))
+        for i in range(PMC_REPS):
+            if workload == "gemm_gate_up":
+                ops.gemm_swiglu_into(*sets[i % 4])
+            else:
+                ops.linear_into(*sets[i % 4])
     elif workload == "decoder":
         from nkilab.model import nki_forward
 
@@ -593,6 +669,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--gemm-shapes", action="store_true", help="only the GEMM shapes beside torch.mm, one JSON line")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--sdpa", action="store_true", help="only attention beside torch SDPA, one JSON line")
+    ap.add_argument("--attention-sweep", action="store_true",
+                    help="only attention time per launch over sizes up to the headline, one JSON line")
     ap.add_argument("--report", default=None, help="write the full result dict as JSON here")
     ap.add_argument("--pmc-pass", metavar="WORKLOAD", help="eager launches of one workload for a rocprofv3 --pmc run")
     ap.add_argument("--collect-counters", metavar="OUT",
@@ -629,6 +708,13 @@ def main() -> int:
     log(f"device: {props.name} CUs={props.multi_processor_count} lib={_lib.LIB_PATH}")
     if args.gemm_shapes:
         print(json.dumps({"gemm_shapes": bench_gemm_shapes(args.steps, args.warmup)}), flush=True)
+        return 0
+    if args.sdpa:
+        print(json.dumps({"attention_beside_torch_sdpa": bench_attention_beside_sdpa(args.steps, args.warmup)}),
+              flush=True)
+        return 0
+    if args.attention_sweep:
+        print(json.dumps({"attention_sweep": bench_attention_sweep(args.steps, args.warmup)}), flush=True)
         return 0
 
     ctr = load_counters()

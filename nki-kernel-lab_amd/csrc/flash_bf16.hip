@@ -134,65 +134,12 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
   const int i16 = lane & 15, g2 = (lane >> 4) & 1;
   const int vfrag_off = L::K_ELEMS + (4 * h32 + (i16 >> 2)) * L::LDV + 16 * g2 + 4 * (i16 & 3);
 
-  // This workgroup's unit range [u0, u1).
   long u0, u1;
-  int vidx = blockIdx.x;
-  if (w.sched == kBalanced) {
-    if (w.grid % 8 == 0) vidx = (blockIdx.x % 8) * (w.grid / 8) + blockIdx.x / 8;  // XCD-contiguous ranges
-    u0 = range_start(vidx, w);
-    u1 = range_start(vidx + 1, w);
-  } else if (w.sched == kPairs) {
-    const int hh = blockIdx.x % p.H, k = blockIdx.x / p.H;
-    u0 = hh * w.units_head + pair_before(k, w);
-    u1 = 2 * k + 2 <= w.nqb ? hh * w.units_head + pair_before(k + 1, w) : (hh + 1) * w.units_head;
-  } else {
-    const int hh = blockIdx.x % p.H;
-    const int b = w.nqb - 1 - blockIdx.x / p.H;  // heaviest first
-    u0 = hh * w.units_head + plain_before(b, w);
-    u1 = u0 + block_tiles(b, w);
-  }
+  const int vidx = wg_range(w, p.H, u0, u1);  // this workgroup's range index and units [u0, u1)
 
-  // A segment: head hh, query block b, tiles [t0, t1) of the block's nt tiles.
-  struct Seg {
-    int hh, b, t0, t1, nt;
-    long bstart;
-  };
-  // The segment of the range that ends with unit u.  A range is walked from
-  // its last segment to its first: the first segment in unit order is often
-  // the tail of a block whose head other workgroups hold, and taking it last
-  // leaves the merge of that block's partial states to this workgroup, the
-  // last to arrive, after its other segments rather than before them.
-  auto decode = [&](long u) __attribute__((always_inline)) {
-    Seg sg;
-    sg.hh = (int)(u / w.units_head);
-    const long r = u - (long)sg.hh * w.units_head;
-    long before;
-    if (w.paired) {
-      const long full = (long)w.tpb * (w.nqb + 1);
-      const long delta = (long)w.tpb * w.nqb - w.last_nt;
-      const int k = min((int)((r + delta) / full), (w.nqb - 1) / 2);
-      before = pair_before(k, w);
-      const int na = block_tiles(k, w);
-      if (r - before < na) {
-        sg.b = k;
-      } else {
-        sg.b = w.nqb - 1 - k;
-        before += na;
-      }
-    } else {
-      int b = (int)((sqrtf(1.0f + 8.0f * (float)r / (float)w.tpb) - 1.0f) * 0.5f);
-      b = max(0, min(b, w.nqb - 1));
-      while (b + 1 <= w.nqb - 1 && plain_before(b + 1, w) <= r) ++b;
-      while (b > 0 && plain_before(b, w) > r) --b;
-      sg.b = b;
-      before = plain_before(b, w);
-    }
-    sg.bstart = (long)sg.hh * w.units_head + before;
-    sg.nt = block_tiles(sg.b, w);
-    sg.t0 = (int)(max(u0, sg.bstart) - sg.bstart);
-    sg.t1 = (int)(u - sg.bstart + 1);
-    return sg;
-  };
+  // The segment of the range that ends with unit u (fsched::decode_seg: a
+  // range is walked from its last segment to its first).
+  auto decode = [&](long u) __attribute__((always_inline)) { return decode_seg(u, u0, w); };
   auto load_q = [&](const Seg& sg, bf16x8 (&q)[NQF]) __attribute__((always_inline)) {
     const bf16* Q = static_cast<const bf16*>(p.q) + (long)sg.hh * p.q_sh;
     const int qrow = QB * sg.b + 32 * wq + l32;
@@ -674,64 +621,11 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
     dv[u] = ok ? 2 * (row * (int)p.v_ss + lc * 8) : 0x40000000;
   }
 
-  // This workgroup's unit range [u0, u1).
   long u0, u1;
-  int vidx = blockIdx.x;
-  if (w.sched == kBalanced) {
-    if (w.grid % 8 == 0) vidx = (blockIdx.x % 8) * (w.grid / 8) + blockIdx.x / 8;
-    u0 = range_start(vidx, w);
-    u1 = range_start(vidx + 1, w);
-  } else if (w.sched == kPairs) {
-    const int hh = blockIdx.x % p.H, k = blockIdx.x / p.H;
-    u0 = hh * w.units_head + pair_before(k, w);
-    u1 = 2 * k + 2 <= w.nqb ? hh * w.units_head + pair_before(k + 1, w) : (hh + 1) * w.units_head;
-  } else {
-    const int hh = blockIdx.x % p.H;
-    const int b = w.nqb - 1 - blockIdx.x / p.H;
-    u0 = hh * w.units_head + plain_before(b, w);
-    u1 = u0 + block_tiles(b, w);
-  }
+  const int vidx = wg_range(w, p.H, u0, u1);  // this workgroup's range index and units [u0, u1)
 
-  struct Seg {
-    int hh, b, t0, t1, nt;
-    long bstart;
-  };
-  // The segment of the range that ends with unit u.  A range is walked from
-  // its last segment to its first: the first segment in unit order is often
-  // the tail of a block whose head other workgroups hold, and taking it last
-  // leaves the merge of that block's partial states to this workgroup, the
-  // last to arrive, after its other segments rather than before them.
-  auto decode = [&](long u) __attribute__((always_inline)) {
-    Seg sg;
-    sg.hh = (int)(u / w.units_head);
-    const long r = u - (long)sg.hh * w.units_head;
-    long before;
-    if (w.paired) {
-      const long full = (long)w.tpb * (w.nqb + 1);
-      const long delta = (long)w.tpb * w.nqb - w.last_nt;
-      const int k = min((int)((r + delta) / full), (w.nqb - 1) / 2);
-      before = pair_before(k, w);
-      const int na = block_tiles(k, w);
-      if (r - before < na) {
-        sg.b = k;
-      } else {
-        sg.b = w.nqb - 1 - k;
-        before += na;
-      }
-    } else {
-      int b = (int)((sqrtf(1.0f + 8.0f * (float)r / (float)w.tpb) - 1.0f) * 0.5f);
-      b = max(0, min(b, w.nqb - 1));
-      while (b + 1 <= w.nqb - 1 && plain_before(b + 1, w) <= r) ++b;
-      while (b > 0 && plain_before(b, w) > r) --b;
-      sg.b = b;
-      before = plain_before(b, w);
-    }
-    sg.bstart = (long)sg.hh * w.units_head + before;
-    sg.nt = block_tiles(sg.b, w);
-    sg.t0 = (int)(max(u0, sg.bstart) - sg.bstart);
-    sg.t1 = (int)(u - sg.bstart + 1);
-    return sg;
-  };
+  // The segment of the range that ends with unit u (fsched::decode_seg).
+  auto decode = [&](long u) __attribute__((always_inline)) { return decode_seg(u, u0, w); };
   bf16x8 qf[QH][NQF];
   auto load_q = [&](const Seg& sg) __attribute__((always_inline)) {
     const bf16* Q = static_cast<const bf16*>(p.q) + (long)sg.hh * p.q_sh;
@@ -1282,6 +1176,22 @@ Work plan(int H, int S, Config cfg) {
     w.grid = H * w.nqb;
   }
   w.cost = w.units + (long)H * w.nqb * w.cpb;
+  // 32-bit schedule arithmetic with magic divisors when every value fits in
+  // an int: the largest are (cost + 1) grid (fsched::range_of) and r + delta
+  // < 2 head_cost <= 2 cost (the pair index), both at most (cost + 1)
+  // max(grid, 2).
+  const long full = (long)w.tpb * (w.nqb + 1);
+  const long fcost = full + 2L * w.cpb;
+  const long head_cost = w.units_head + (long)w.nqb * w.cpb;
+  w.fast = (w.cost + 1) * (long)(w.grid > 2 ? w.grid : 2) < (1L << 31);
+  if (w.fast) {
+    w.dv_units_head = make_div32((unsigned)w.units_head);
+    w.dv_full = make_div32((unsigned)full);
+    w.dv_fcost = make_div32((unsigned)fcost);
+    w.dv_head_cost = make_div32((unsigned)head_cost);
+    w.dv_grid = make_div32((unsigned)w.grid);
+    w.dv_cost = make_div32((unsigned)w.cost);
+  }
   return w;
 }
 

@@ -41,6 +41,31 @@ constexpr float kRescaleSlack = 8.0f;
 
 enum Sched { kBlock = 0, kBalanced = 1, kPairs = 2 };
 
+// Division of n (0 <= n < 2^32) by a per-launch constant d (1 <= d < 2^32) as
+// a multiply-high, an add and two shifts (Granlund and Montgomery, "Division
+// by invariant integers using multiplication", PLDI 1994, fig. 4.1): the
+// workgroups' schedule arithmetic divides by a handful of launch constants,
+// and a 32-bit division otherwise costs ~35 instructions with a VALU round
+// trip, a 64-bit one ~100.
+struct Div32 {
+  unsigned d, m;
+  int sh1, sh2;
+};
+inline Div32 make_div32(unsigned d) {
+  int l = 0;  // ceil(log2 d)
+  while (l < 32 && (1ull << l) < d) ++l;
+  Div32 f;
+  f.d = d;
+  f.m = (unsigned)(((1ull << 32) * ((1ull << l) - d)) / d + 1);
+  f.sh1 = l < 1 ? l : 1;
+  f.sh2 = l > 1 ? l - 1 : 0;
+  return f;
+}
+__host__ __device__ inline unsigned div32(const Div32& f, unsigned n) {
+  const unsigned t = (unsigned)(((unsigned long long)f.m * n) >> 32);
+  return (t + ((n - t) >> f.sh1)) >> f.sh2;
+}
+
 struct Work {
   int nqb;          // query blocks per head
   int tpb;          // key tiles added per block (QB / BN): block b has tpb (b + 1)
@@ -55,26 +80,46 @@ struct Work {
   float* part;      // balanced: partial states
   int part_bytes;   // balanced: bytes of part
   int* count;       // balanced: arrival counters [H][nqb], zero between calls
+  // Magic divisors of the launch constants below, valid when fast is set
+  // (every dividend of the schedule arithmetic fits in 32 bits): units_head,
+  // the pair span tpb (nqb + 1), its cost tpb (nqb + 1) + 2 cpb, the head
+  // cost, grid and cost.
+  int fast;
+  Div32 dv_units_head, dv_full, dv_fcost, dv_head_cost, dv_grid, dv_cost;
 };
 
 // a / b for 0 <= a, 0 < b: a 32-bit division when both fit (every realistic
 // shape), which is a few instructions instead of the ~100 of a 64-bit one.
-__device__ __forceinline__ long udiv(long a, long b) {
+__host__ __device__ __forceinline__ long udiv(long a, long b) {
   if (((unsigned long)a | (unsigned long)b) >> 32 == 0) return (long)((unsigned)a / (unsigned)b);
   return a / b;
 }
 
-__device__ __forceinline__ int block_tiles(int b, const Work& w) {
+// The schedule arithmetic below is written once over an integer type I: int
+// when the launch's values fit (Work::fast: every dividend below 2^32, every
+// quantity below 2^31), with the magic divisors, so that a workgroup's
+// set-up runs a short chain of 32-bit scalar instructions; long otherwise.
+// q(a, f, b) is a / b for the launch constant b whose magic divisor is f.
+template <typename I>
+__host__ __device__ __forceinline__ I q(I a, const Div32& f, long b);
+template <>
+__host__ __device__ __forceinline__ int q<int>(int a, const Div32& f, long) { return (int)div32(f, (unsigned)a); }
+template <>
+__host__ __device__ __forceinline__ long q<long>(long a, const Div32&, long b) { return udiv(a, b); }
+
+__host__ __device__ __forceinline__ int block_tiles(int b, const Work& w) {
   return b == w.nqb - 1 ? w.last_nt : w.tpb * (b + 1);
 }
 // Block order: units of a head before block b.
-__device__ __forceinline__ long plain_before(int b, const Work& w) { return (long)w.tpb * b * (b + 1) / 2; }
+template <typename I = long>
+__host__ __device__ __forceinline__ I plain_before(int b, const Work& w) { return (I)w.tpb * b * (b + 1) / 2; }
 // Pair order: units of a head before pair k (blocks k and n-1-k).  Every pair
 // but the first holds tpb (n + 1) units; the first lacks the last block's
 // missing tiles (tpb n - last_nt).
-__device__ __forceinline__ long pair_before(int k, const Work& w) {
-  const long full = (long)w.tpb * (w.nqb + 1);
-  const long delta = (long)w.tpb * w.nqb - w.last_nt;
+template <typename I = long>
+__host__ __device__ __forceinline__ I pair_before(int k, const Work& w) {
+  const I full = (I)w.tpb * (w.nqb + 1);
+  const I delta = (I)w.tpb * w.nqb - w.last_nt;
   return k == 0 ? 0 : k * full - delta;
 }
 
@@ -86,40 +131,55 @@ __device__ __forceinline__ long pair_before(int k, const Work& w) {
 // [k F - delta, (k + 1) F - delta) with F = tpb (n + 1) + 2 cpb (pair 0 from 0):
 // cpb, block k's units, cpb, block n-1-k's units.  A range of more than cpb
 // cost holds at least one unit, which the planner guarantees.
-__device__ __forceinline__ long head_cost(const Work& w) { return w.units_head + (long)w.nqb * w.cpb; }
+template <typename I = long>
+__host__ __device__ __forceinline__ I head_cost(const Work& w) { return (I)w.units_head + (I)w.nqb * w.cpb; }
 
 // Units (in pair order) whose cost position is below c.
-__device__ __forceinline__ long units_below_cost(long c, const Work& w) {
-  const long hc = head_cost(w);
-  const long hh = udiv(c, hc);
-  const long r = c - hh * hc;
-  const long F = (long)w.tpb * (w.nqb + 1) + 2L * w.cpb;
-  const long delta = (long)w.tpb * w.nqb - w.last_nt;
-  const int k = (int)min(udiv(r + delta, F), (long)((w.nqb - 1) / 2));
-  const long o = r - (k == 0 ? 0 : k * F - delta);
-  const long na = block_tiles(k, w);
-  const long in_pair = o < w.cpb + na ? max(0L, o - w.cpb) : na + max(0L, o - 2L * w.cpb - na);
-  return hh * w.units_head + pair_before(k, w) + in_pair;
+template <typename I>
+__host__ __device__ __forceinline__ I units_below_cost_t(I c, const Work& w) {
+  const I hc = head_cost<I>(w);
+  const I hh = q<I>(c, w.dv_head_cost, hc);
+  const I r = c - hh * hc;
+  const I F = (I)w.tpb * (w.nqb + 1) + 2 * (I)w.cpb;
+  const I delta = (I)w.tpb * w.nqb - w.last_nt;
+  const I kq = q<I>(r + delta, w.dv_fcost, F);
+  const int k = (int)(kq < (I)((w.nqb - 1) / 2) ? kq : (I)((w.nqb - 1) / 2));
+  const I o = r - (k == 0 ? 0 : k * F - delta);
+  const I na = block_tiles(k, w);
+  const I in_pair = o < w.cpb + na ? (o > w.cpb ? o - w.cpb : 0) : na + (o > 2 * (I)w.cpb + na ? o - 2 * (I)w.cpb - na : 0);
+  return hh * (I)w.units_head + pair_before<I>(k, w) + in_pair;
 }
 
 // Cost position of unit u.
-__device__ __forceinline__ long cost_of_unit(long u, const Work& w) {
-  const long hh = udiv(u, w.units_head);
-  const long r = u - hh * w.units_head;
-  const long full = (long)w.tpb * (w.nqb + 1);
-  const long delta = (long)w.tpb * w.nqb - w.last_nt;
-  const int k = (int)min(udiv(r + delta, full), (long)((w.nqb - 1) / 2));
-  const long starts = r - pair_before(k, w) < block_tiles(k, w) ? 2 * k + 1 : 2 * k + 2;
-  return hh * head_cost(w) + r + starts * w.cpb;
+template <typename I>
+__host__ __device__ __forceinline__ I cost_of_unit_t(I u, const Work& w) {
+  const I hh = q<I>(u, w.dv_units_head, w.units_head);
+  const I r = u - hh * (I)w.units_head;
+  const I full = (I)w.tpb * (w.nqb + 1);
+  const I delta = (I)w.tpb * w.nqb - w.last_nt;
+  const I kq = q<I>(r + delta, w.dv_full, full);
+  const int k = (int)(kq < (I)((w.nqb - 1) / 2) ? kq : (I)((w.nqb - 1) / 2));
+  const I starts = r - pair_before<I>(k, w) < block_tiles(k, w) ? 2 * k + 1 : 2 * k + 2;
+  return hh * head_cost<I>(w) + r + starts * w.cpb;
 }
 
 // First unit of balanced range v (v = grid: the end of the last range).
-__device__ __forceinline__ long range_start(long v, const Work& w) { return units_below_cost(udiv(v * w.cost, w.grid), w); }
+template <typename I>
+__host__ __device__ __forceinline__ I range_start_t(I v, const Work& w) {
+  return units_below_cost_t<I>(q<I>(v * (I)w.cost, w.dv_grid, w.grid), w);
+}
+__host__ __device__ __forceinline__ long range_start(long v, const Work& w) {
+  return w.fast ? (long)range_start_t<int>((int)v, w) : range_start_t<long>(v, w);
+}
 
 // The balanced range that holds unit u: the one whose cost interval
 // [v cost / grid, (v + 1) cost / grid) holds u's cost position.
-__device__ __forceinline__ int range_of(long u, const Work& w) {
-  return (int)udiv((cost_of_unit(u, w) + 1) * w.grid - 1, w.cost);
+template <typename I>
+__host__ __device__ __forceinline__ int range_of_t(I u, const Work& w) {
+  return (int)q<I>((cost_of_unit_t<I>(u, w) + 1) * (I)w.grid - 1, w.dv_cost, w.cost);
+}
+__host__ __device__ __forceinline__ int range_of(long u, const Work& w) {
+  return w.fast ? range_of_t<int>((int)u, w) : range_of_t<long>(u, w);
 }
 
 // This workgroup's range index and unit range [u0, u1).  Balanced ranges are
@@ -158,16 +218,18 @@ struct Seg {
 // often the tail of a block whose head other workgroups hold, and taking it
 // last leaves the merge of that block's partial states to this workgroup,
 // the last to arrive, after its other segments rather than before them.
-__device__ __forceinline__ Seg decode_seg(long u, long u0, const Work& w) {
+template <typename I>
+__host__ __device__ __forceinline__ Seg decode_seg_t(I u, I u0, const Work& w) {
   Seg sg;
-  sg.hh = (int)udiv(u, w.units_head);
-  const long r = u - (long)sg.hh * w.units_head;
-  long before;
+  sg.hh = (int)q<I>(u, w.dv_units_head, w.units_head);
+  const I r = u - (I)sg.hh * (I)w.units_head;
+  I before;
   if (w.paired) {
-    const long full = (long)w.tpb * (w.nqb + 1);
-    const long delta = (long)w.tpb * w.nqb - w.last_nt;
-    const int k = min((int)udiv(r + delta, full), (w.nqb - 1) / 2);
-    before = pair_before(k, w);
+    const I full = (I)w.tpb * (w.nqb + 1);
+    const I delta = (I)w.tpb * w.nqb - w.last_nt;
+    const I kq = q<I>(r + delta, w.dv_full, full);
+    const int k = (int)(kq < (I)((w.nqb - 1) / 2) ? kq : (I)((w.nqb - 1) / 2));
+    before = pair_before<I>(k, w);
     const int na = block_tiles(k, w);
     if (r - before < na) {
       sg.b = k;
@@ -178,16 +240,20 @@ __device__ __forceinline__ Seg decode_seg(long u, long u0, const Work& w) {
   } else {
     int b = (int)((sqrtf(1.0f + 8.0f * (float)r / (float)w.tpb) - 1.0f) * 0.5f);
     b = max(0, min(b, w.nqb - 1));
-    while (b + 1 <= w.nqb - 1 && plain_before(b + 1, w) <= r) ++b;
-    while (b > 0 && plain_before(b, w) > r) --b;
+    while (b + 1 <= w.nqb - 1 && plain_before<I>(b + 1, w) <= r) ++b;
+    while (b > 0 && plain_before<I>(b, w) > r) --b;
     sg.b = b;
-    before = plain_before(b, w);
+    before = plain_before<I>(b, w);
   }
-  sg.bstart = (long)sg.hh * w.units_head + before;
+  const I bstart = (I)sg.hh * (I)w.units_head + before;
+  sg.bstart = bstart;
   sg.nt = block_tiles(sg.b, w);
-  sg.t0 = (int)(max(u0, sg.bstart) - sg.bstart);
-  sg.t1 = (int)(u - sg.bstart + 1);
+  sg.t0 = (int)((u0 > bstart ? u0 : bstart) - bstart);
+  sg.t1 = (int)(u - bstart + 1);
   return sg;
+}
+__host__ __device__ __forceinline__ Seg decode_seg(long u, long u0, const Work& w) {
+  return w.fast ? decode_seg_t<int>((int)u, (int)u0, w) : decode_seg_t<long>(u, u0, w);
 }
 
 // The workgroup holding a split block's last range merges it.  It walks that
