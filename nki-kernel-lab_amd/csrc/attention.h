@@ -32,7 +32,9 @@ struct Work;
 // The 64-key-tile bf16 kernel (flash_fwd.hip) for 64 < d <= 128: launch over
 // a planned Work (128-query blocks, 64-key tiles), and the bytes of one
 // workgroup's partial state of a block (the workspace holds two per range).
-void launch_flash_fwd(const AttnArgs& a, const fsched::Work& w, hipStream_t st);
+// pingpong: the two key-half wavefronts of a SIMD half an iteration apart
+// (matrix-core work of one beside vector work of the other).
+void launch_flash_fwd(const AttnArgs& a, const fsched::Work& w, bool pingpong, hipStream_t st);
 size_t flash_fwd_part_bytes();
 // Process-wide kernel / schedule / block / start-cost overrides (-1: automatic).
 int flash_bf16_configure(int kern, int sched, int qb, int cpb);

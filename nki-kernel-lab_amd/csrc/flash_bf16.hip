@@ -1068,7 +1068,7 @@ int cu_count() {
 // (256 registers each, two independent workgroups per CU); or the
 // 64-key-tile kernel of flash_fwd.hip (kFwd: 128-query blocks, two
 // wavefronts per SIMD splitting each tile's keys, LDS-DMA stages).
-enum Kern { kTeams = 0, kW32x4 = 1, kW64x2 = 2, kW64x4 = 3, kTeams4 = 4, kW32x4x2 = 5, kFwd = 6 };
+enum Kern { kTeams = 0, kW32x4 = 1, kW64x2 = 2, kW64x4 = 3, kTeams4 = 4, kW32x4x2 = 5, kFwd = 6, kFwdPP = 7 };
 
 // Launch-configuration overrides (-1: the automatic choice), process-wide:
 // read from the environment once, at first use -- NKL_FLASH_SCHEDULE=
@@ -1099,6 +1099,7 @@ Overrides& overrides() {
       if (!strcmp(f, "w64")) r.kern = kW64x2;
       if (!strcmp(f, "w64x4")) r.kern = kW64x4;
       if (!strcmp(f, "fwd")) r.kern = kFwd;
+      if (!strcmp(f, "pp")) r.kern = kFwdPP;
     }
     if (const char* f = getenv("NKL_FLASH_CPB")) r.cpb = min(max(atoi(f), 0), 4096);
     return r;
@@ -1109,7 +1110,7 @@ Overrides& overrides() {
 }  // namespace
 
 int flash_bf16_configure(int kern, int sched, int qb, int cpb) {
-  if (kern < -1 || kern > kFwd || sched < -1 || sched > kPairs || (qb != -1 && qb != 64 && qb != 128) || cpb < -1 ||
+  if (kern < -1 || kern > kFwdPP || sched < -1 || sched > kPairs || (qb != -1 && qb != 64 && qb != 128) || cpb < -1 ||
       cpb > 4096)
     return set_error(NKL_EINVAL, "nkl_flash_attn_configure: kernel %d, schedule %d, qb %d, cpb %d out of range", kern,
                      sched, qb, cpb);
@@ -1139,7 +1140,8 @@ int wgs_per_cu(int kern) { return kern == kW64x2 || kern == kTeams4 || kern == k
 
 Work plan(int H, int S, Config cfg) {
   Work w{};
-  const int bn = cfg.kern == kFwd ? 64 : BN;  // keys per tile
+  const bool fwd = cfg.kern == kFwd || cfg.kern == kFwdPP;
+  const int bn = fwd ? 64 : BN;  // keys per tile
   w.tpb = cfg.qb / bn;
   w.nqb = (S + cfg.qb - 1) / cfg.qb;
   w.last_nt = (S - 1) / bn + 1;
@@ -1166,7 +1168,7 @@ Work plan(int H, int S, Config cfg) {
     const bool pipelined = cfg.kern == kW32x4 || cfg.kern == kW64x2 || cfg.kern == kW64x4 || cfg.kern == kW32x4x2;
     const long nblocks = (long)H * w.nqb;
     const bool few = nblocks < w.grid;
-    int cpb = cfg.kern == kFwd ? 4 : pipelined ? 2 : cfg.qb == 64 ? (few ? 14 : 10) : (few ? 12 : 4);
+    int cpb = fwd ? 4 : pipelined ? 2 : cfg.qb == 64 ? (few ? 14 : 10) : (few ? 12 : 4);
     if (overrides().cpb >= 0) cpb = overrides().cpb;
     while (cpb > 0 && (w.units + nblocks * cpb) / w.grid < cpb + 1) --cpb;
     w.cpb = cpb < 0 ? 0 : cpb;
@@ -1218,7 +1220,8 @@ Config choose(int H, int S, int d) {
   if (ov.qb >= 0) cfg.qb = ov.qb;
   if (ov.kern >= 0) cfg.kern = ov.kern;
   if (d <= 64 && cfg.kern != kTeams4) cfg.kern = kTeams;
-  if (cfg.kern == kW32x4 || cfg.kern == kW64x2 || cfg.kern == kW32x4x2 || cfg.kern == kFwd) cfg.qb = 128;
+  if (cfg.kern == kW32x4 || cfg.kern == kW64x2 || cfg.kern == kW32x4x2 || cfg.kern == kFwd || cfg.kern == kFwdPP)
+    cfg.qb = 128;
   if (cfg.kern == kW64x4) cfg.qb = 256;
   return cfg;
 }
@@ -1232,7 +1235,7 @@ size_t part_floats(int qb) {
 }
 
 size_t part_floats_for(int d, const Config& cfg) {
-  if (cfg.kern == kFwd) return flash_fwd_part_bytes() / 4;
+  if (cfg.kern == kFwd || cfg.kern == kFwdPP) return flash_fwd_part_bytes() / 4;
   return d <= 32 ? part_floats<32>(cfg.qb) : d <= 64 ? part_floats<64>(cfg.qb) : part_floats<128>(cfg.qb);
 }
 
@@ -1293,8 +1296,8 @@ int flash_bf16_launch(const AttnArgs& a, void* workspace, size_t workspace_bytes
     w.part_bytes = (int)need;
     w.count = counters;
   }
-  if (cfg.kern == kFwd) {
-    launch_flash_fwd(a, w, st);
+  if (cfg.kern == kFwd || cfg.kern == kFwdPP) {
+    launch_flash_fwd(a, w, cfg.kern == kFwdPP, st);
     return check_launch("nkl_flash_attn_causal");
   }
   if (cfg.kern == kW32x4 || cfg.kern == kW64x2 || cfg.kern == kW64x4 || cfg.kern == kW32x4x2) {

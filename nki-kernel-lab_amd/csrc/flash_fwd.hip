@@ -87,6 +87,7 @@ using I = std::integral_constant<int, N>;
 
 }  // namespace
 
+template <bool PP>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void flash_fwd_kernel(AttnArgs p, Work w) {
   using namespace fwd;
@@ -203,12 +204,14 @@ void flash_fwd_kernel(AttnArgs p, Work w) {
     const int nw = __builtin_amdgcn_readfirstlane(max(0, min(nt, lastj + 1)));
     const bool diag_in = ((qi - kh) & 1) == 0 && lastj >= 0 && lastj < nt;  // tile nw - 1 is the diagonal one
 
-    if (nt > 1)
-      wait_vm<4>();  // Q and tile 0 have landed
-    else
-      wait_vm<0>();
-    bar();
-    if (nt > 2) dma(src, 2);
+    if constexpr (!PP) {
+      if (nt > 1)
+        wait_vm<4>();  // Q and tile 0 have landed
+      else
+        wait_vm<0>();
+      bar();
+      if (nt > 2) dma(src, 2);
+    }
 
     float m_run = -INFINITY, l_run = 0.f;
     floatx16 oacc[4];
@@ -260,6 +263,7 @@ void flash_fwd_kernel(AttnArgs p, Work w) {
       }
     };
 
+    if constexpr (!PP) {
     floatx16 s_cur;
     bf16x8 va[4][2];  // V^T fragments of the tile being multiplied (read one step ahead)
     if (nw > 0) {
@@ -384,6 +388,205 @@ void flash_fwd_kernel(AttnArgs p, Work w) {
       iter(I<2>{}, j + 2);
       if (j + 3 >= nt) break;
       iter(I<3>{}, j + 3);
+    }
+
+    } else {
+      // ---- ping-pong: the two wavefronts of a SIMD (key halves kh = 0, 1 of
+      // every tile, same queries) run the same work per tile -- P V and
+      // S = K Q^T on the matrix cores (16 MFMAs), the online softmax on the
+      // vector ALUs -- half an iteration apart.  After the barrier of
+      // iteration j, kh = 0 issues its MFMAs (P V of tile j-1, S of tile j)
+      // while kh = 1 runs the softmax of tile j-1 and reads its MFMA operands
+      // (V of tile j-1, K of tile j) from LDS; then kh = 1 issues its MFMAs
+      // while kh = 0 runs the softmax of tile j and reads V of tile j and K of
+      // tile j+1.  One wavefront on the matrix cores beside one on the vector
+      // ALUs keeps both busy (a wavefront interleaving the two kinds itself
+      // hides about half its vector work), and each half-iteration carries
+      // half of the LDS fragment reads.  K tiles are therefore copied one tile
+      // further ahead than V tiles: iteration j needs K of tiles j, j+1 and V
+      // of tiles j-1, j, and refills the K stage of tile j-1 with tile j+3 and
+      // the V stage of tile j-2 with tile j+2 (tile t in stage t % 4 of each).
+      floatx16 sc;
+      bf16x8 pf[2], va[4][2], kf[8];
+      // Masks keys after each lane's query in the scores sc of tile jt (first
+      // key 64 (t0 + jt) + 32 kh), raises the running max lazily and leaves
+      // the bf16 probabilities in pf.
+      auto softmax = [&](int jt) __attribute__((always_inline)) {
+        const int dlt = 64 * (t0 + jt) + 32 * kh - qw;  // first key - first query: 0 on the diagonal
+        float mx;
+        if (dlt > -32) {
+          mx = -INFINITY;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            sc[e] = dlt + 8 * (e >> 2) + 4 * h32 + (e & 3) > l32 ? -INFINITY : sc[e];
+            mx = fmaxf(mx, sc[e]);
+          }
+        } else {
+          mx = plain_max(sc);
+        }
+        rescale(mx);
+        const float mneg = m_run == -INFINITY ? 0.f : -m_run;
+        float rs = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const float pe = fast_exp2(fmaf(sc[e], c, mneg));
+          rs += pe;
+          pf[e >> 3][e & 7] = (bf16)pe;
+        }
+        l_run += rs;
+      };
+      auto pv = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int uu = 0; uu < 2; ++uu) oacc[db] = MF::mma(va[db][uu], pf[uu], oacc[db]);
+      };
+      auto qk = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sc[e] = 0.f;
+#pragma unroll
+        for (int f = 0; f < 8; ++f) sc = MF::mma(kf[f], qf[f], sc);
+      };
+      auto read_k = [&](auto st_c) __attribute__((always_inline)) {
+        constexpr int st = decltype(st_c)::value;
+#pragma unroll
+        for (int f = 0; f < 8; ++f) kf[f] = kfrag(st, f);
+      };
+      auto read_v = [&](auto st_c) __attribute__((always_inline)) {
+        constexpr int st = decltype(st_c)::value;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int uu = 0; uu < 2; ++uu) va[db][uu] = vfrag(st, db, uu);
+      };
+      // Copies of K (or V) of tile t into its stage st = t % 4: two 1 KB
+      // copies per wavefront, through a buffer resource over the tile's rows
+      // (rows past the sequence read as zeros).  (One resource per segment
+      // with the tile offset in the per-lane offset was measured slower:
+      // 8 x 2048 25.8 -> 30.3 us, 8 x 8192 150 -> 156 us.)
+      auto dma_k = [&](auto st_c, int t) __attribute__((always_inline)) {
+        constexpr int st = decltype(st_c)::value;
+        const int nkeys = min(BN, src.keys - t * BN);
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(src.k + (long)t * BN * p.k_ss), (short)0, 2 * ((nkeys - 1) * (int)p.k_ss + dlim), kBufferFlags);
+        const unsigned sb = lds0 + st * TILEB;
+        copy_1k(rk, dk[0], sb);
+        copy_1k(rk, dk[1], sb + 1024);
+      };
+      auto dma_v = [&](auto st_c, int t) __attribute__((always_inline)) {
+        constexpr int st = decltype(st_c)::value;
+        const int nkeys = min(BN, src.keys - t * BN);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(src.v + (long)t * BN * p.v_ss), (short)0, 2 * ((nkeys - 1) * (int)p.v_ss + dlim), kBufferFlags);
+        const unsigned sb = lds0 + VOFF + st * TILEB;
+        copy_1k(rv, dv[0], sb);
+        copy_1k(rv, dv[1], sb + 1024);
+      };
+      // Top of iteration j: K of tile j+1 and V of tile j have landed for
+      // every wavefront (the copies issued after them are those of the
+      // previous iteration: K of tile j+2 and V of tile j+1), every wavefront
+      // is done with the K stage of tile j-1 and the V stage of tile j-2.
+      auto top = [&](int j) __attribute__((always_inline)) {
+        if (j + 2 < nt)
+          wait_vm<4>();
+        else if (j + 1 < nt)
+          wait_vm<2>();
+        else
+          wait_vm<0>();
+        bar();
+      };
+      // The copies of iteration j (K of tile j+3 and V of tile j+2 into the
+      // stages top(j) freed).  Each wavefront issues its share at the start
+      // of its vector half: a burst of copies holds a wavefront's issue while
+      // the vector memory unit takes them (32 KB per CU), which would delay
+      // the MFMAs of the wavefront whose matrix half comes first.
+      auto copies = [&](auto st_c, int j) __attribute__((always_inline)) {
+        constexpr int st = decltype(st_c)::value;
+        if (j + 3 < nt) dma_k(I<(st + 3) % 4>{}, j + 3);
+        if (j + 2 < nt) dma_v(I<(st + 2) % 4>{}, j + 2);
+      };
+      // One iteration j >= 1 (st = j % 4, a compile-time constant).
+      auto body0 = [&](auto st_c, int j) __attribute__((always_inline)) {
+        constexpr int st = decltype(st_c)::value;
+        top(j);
+        pv();
+        qk();
+        __builtin_amdgcn_sched_barrier(0);
+        copies(I<st>{}, j);
+        read_v(I<st>{});
+        if (j + 1 < nt) read_k(I<(st + 1) % 4>{});
+        softmax(j);
+        __builtin_amdgcn_sched_barrier(0);
+      };
+      auto body1 = [&](auto st_c, int j) __attribute__((always_inline)) {
+        constexpr int st = decltype(st_c)::value;
+        top(j);
+        copies(I<st>{}, j);
+        read_v(I<(st + 3) % 4>{});
+        read_k(I<st>{});
+        softmax(j - 1);
+        __builtin_amdgcn_sched_barrier(0);
+        pv();
+        qk();
+        __builtin_amdgcn_sched_barrier(0);
+      };
+      auto run = [&](auto body, auto kh_c) __attribute__((always_inline)) {
+        // Tile 0: S only (kh = 0 also its softmax, V of tile 0 and K of tile
+        // 1).  The segment's first two tiles were copied before the previous
+        // segment's hand-over (stages 0 and 1); stages 2 and 3 held that
+        // hand-over, so their copies wait for the barrier.  Every copy issued
+        // after K of tile 1 is V of tile 1 (or a store of the previous segment,
+        // which this wait also covers).
+        if (nt > 1)
+          wait_vm<2>();
+        else
+          wait_vm<0>();
+        bar();
+        auto copies0 = [&]() __attribute__((always_inline)) {
+          if (nt > 2) dma_k(I<2>{}, 2);
+          copies(I<0>{}, 0);
+        };
+        if constexpr (decltype(kh_c)::value == 1) copies0();
+        read_k(I<0>{});
+        __builtin_amdgcn_sched_barrier(0);
+        qk();
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (decltype(kh_c)::value == 0) {
+          copies0();
+          read_v(I<0>{});
+          if (nt > 1) read_k(I<1>{});
+          softmax(0);
+        }
+        int j = 1;
+#pragma unroll 1
+        for (; j + 4 <= nt; j += 4) {
+          body(I<1>{}, j);
+          body(I<2>{}, j + 1);
+          body(I<3>{}, j + 2);
+          body(I<0>{}, j + 3);
+        }
+        if (j < nt) {
+          body(I<1>{}, j);
+          if (j + 1 < nt) {
+            body(I<2>{}, j + 1);
+            if (j + 2 < nt) body(I<3>{}, j + 2);
+          }
+        }
+      };
+      if (kh == 0) {
+        run(body0, I<0>{});
+        pv();  // P V of the last tile (its V^T fragments are in va)
+      } else {
+        run(body1, I<1>{});
+        // softmax and P V of the last tile, from stage (nt - 1) % 4
+        const int sl = (nt - 1) & 3;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int uu = 0; uu < 2; ++uu) va[db][uu] = vfrag(sl, db, uu);
+        softmax(nt - 1);
+        pv();
+      }
     }
 
     // ---- segment end.  The next segment's Q and first two tiles are
@@ -588,8 +791,11 @@ void flash_fwd_kernel(AttnArgs p, Work w) {
   }
 }
 
-void launch_flash_fwd(const AttnArgs& a, const Work& w, hipStream_t st) {
-  flash_fwd_kernel<<<dim3((unsigned)w.grid), dim3(512), 0, st>>>(a, w);
+void launch_flash_fwd(const AttnArgs& a, const Work& w, bool pingpong, hipStream_t st) {
+  if (pingpong)
+    flash_fwd_kernel<true><<<dim3((unsigned)w.grid), dim3(512), 0, st>>>(a, w);
+  else
+    flash_fwd_kernel<false><<<dim3((unsigned)w.grid), dim3(512), 0, st>>>(a, w);
 }
 
 size_t flash_fwd_part_bytes() { return fwd::PART_BYTES; }

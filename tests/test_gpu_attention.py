@@ -143,7 +143,7 @@ def test_flash_bf16_schedules(rng, flash_cfg, kernel, qb, schedule, H, S, d):
     np.testing.assert_allclose(out[:, 0], _np(v)[:, 0], rtol=2 ** -8, atol=0)  # query 0 sees only key 0
 
 
-@pytest.mark.parametrize("kernel", ["w1", "w1o2", "w64", "w64x4", "fwd"])
+@pytest.mark.parametrize("kernel", ["w1", "w1o2", "w64", "w64x4", "fwd", "pp"])
 @pytest.mark.parametrize("schedule", ["balanced", "pairs", "block"])
 @pytest.mark.parametrize("H,S,d", [(1, 1, 128), (3, 77, 128), (1, 300, 128), (2, 1537, 128), (5, 640, 96),
                                    (1, 129, 128), (2, 4096, 128), (4, 257, 72)])
@@ -160,7 +160,7 @@ def test_flash_bf16_one_wave_per_simd_kernel(rng, flash_cfg, kernel, schedule, H
     np.testing.assert_allclose(out[:, 0], _np(v)[:, 0], rtol=2 ** -8, atol=0)
 
 
-@pytest.mark.parametrize("kernel", ["w1", "w1o2", "w64", "w64x4", "teams4", "fwd"])
+@pytest.mark.parametrize("kernel", ["w1", "w1o2", "w64", "w64x4", "teams4", "fwd", "pp"])
 def test_flash_bf16_one_wave_per_simd_config(flash_cfg, kernel):
     """8 x 2048 x 128 through each one-wavefront-per-SIMD kernel (balanced):
     within 3e-3 of fp32 SDPA."""
@@ -184,7 +184,7 @@ def test_flash_bf16_schedules_agree_on_config(flash_cfg, qb, schedule):
 
 
 @pytest.mark.parametrize("kernel,qb", [("teams", "64"), ("teams", "128"), ("teams4", "64"), ("w1o2", "128"),
-                                       ("fwd", "128")])
+                                       ("fwd", "128"), ("pp", "128")])
 @pytest.mark.parametrize("cpb", ["0", "3", "15", "1000"])
 @pytest.mark.parametrize("H,S,d", [(8, 2048, 128), (3, 1537, 128), (5, 300, 64), (16, 640, 96)])
 def test_flash_bf16_balanced_block_start_cost(rng, flash_cfg, kernel, qb, cpb, H, S, d):
@@ -305,7 +305,8 @@ def test_gqa_attention_matches_sdpa_on_repeated_kv(rng, variant, H, Hkv, S, d):
 @pytest.mark.parametrize("kernel,qb,schedule", [("teams", "128", "balanced"), ("teams", "64", "balanced"),
                                                 ("teams", "128", "pairs"), ("teams", "128", "block"),
                                                 ("w64", "128", "balanced"), ("teams4", "64", "balanced"),
-                                                ("fwd", "128", "balanced"), ("fwd", "128", "pairs")])
+                                                ("fwd", "128", "balanced"), ("fwd", "128", "pairs"),
+                                                ("pp", "128", "balanced"), ("pp", "128", "pairs")])
 def test_gqa_bf16_every_kernel_and_schedule(rng, flash_cfg, kernel, qb, schedule):
     from nkilab import ops
 
