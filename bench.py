@@ -8,8 +8,9 @@ Prints ONE JSON line.  The headline (``value``) is causal attention at
 4*H*d*S(S+1)/2.  The same line carries every other benchmark configuration,
 each with its own roofline object: the fused softmax / RMSNorm / SwiGLU at
 4096 x 2048 bf16 (HBM GB/s), the 1024^3 bf16 matmul, causal attention at
-1 x 4096 and 32 x 16384, and the decoder block (the configuration that meets
-1e-3 against the fp32 block, with the all-bf16 one beside it).
+1 x 4096 and 32 x 16384, and the decoder block (the fp16 configuration, which
+meets 1e-3 against the fp32 block, with the all-bf16 and split-operand ones
+beside it).
 
 Timing: every kernel is launched from a captured HIP graph (so host launch
 overhead does not leave the GPU idle between launches), replayed K times
@@ -311,9 +312,10 @@ def bench_gemm_shapes(reps, warmup):
 
 
 def bench_decoder(reps, warmup, counters=None):
-    """The decoder block (config 5): the split-operand configuration, which
-    meets 1e-3 against the fp32 block and is the one reported, and the
-    all-bf16 configuration beside it; each with its measured error."""
+    """The decoder block (config 5): the fp16 configuration, which meets 1e-3
+    against the fp32 block at the bf16 path's cost and is the one reported;
+    the all-bf16 configuration (over 1e-3) and the split-operand one (fp32
+    accurate, 2.7x the time) beside it; each with its measured error."""
     import torch
 
     from nkilab import workloads
@@ -325,23 +327,23 @@ def bench_decoder(reps, warmup, counters=None):
     with torch.no_grad():
         ref = block(xg)
     flops = workloads.decoder_flops()
+    seven = "7 launches: 2 RMSNorm, QKV, attention, out-proj, fused gate/up/SwiGLU, down-proj"
     out = {}
-    for name, cd, launches in (("split", "split", "13 launches: 2 RMSNorm, 4 hi/lo splits, 5 bf16 GEMMs over K-doubled "
-                                                  "operands, fp32 attention, SwiGLU"),
-                               ("bf16", "bfloat16", "7 launches: 2 RMSNorm, QKV, attention, out-proj, fused "
-                                                    "gate/up/SwiGLU, down-proj")):
+    for name, cd, launches in (("fp16", "float16", seven), ("bf16", "bfloat16", seven),
+                               ("split", "split", "13 launches: 2 RMSNorm, 4 hi/lo splits, 5 bf16 GEMMs over K-doubled "
+                                                  "operands, fp32 attention, SwiGLU")):
         y = nki_forward(block, xg, compute_dtype=cd)  # fills the weight cache and the attention scratch
         torch.cuda.synchronize()
         err = float((y.float() - ref).abs().max() / ref.abs().max())
         sec = time_launches([lambda cd=cd: nki_forward(block, xg, compute_dtype=cd)], reps, warmup)
         out[name] = {"us": round(sec * 1e6, 3), "tflops": round(flops / sec / 1e12, 3),
                      "rel_err_vs_fp32_block": err, "launches": launches}
-    rep = out["split"]
+    rep = out["fp16"]
     return {"us": rep["us"], "tflops": rep["tflops"], "rel_err_vs_fp32_block": rep["rel_err_vs_fp32_block"],
-            "compute": "split: fp32 activations and residual, projections on bf16 MFMA over hi/lo operand pairs, "
-                       "fp32 attention",
+            "compute": "fp16 activations and weights (fp32 accumulation, fp32 residual stream), P rounded to fp16",
             "roofline": roofline("mfma", rep["tflops"], "TFLOP/s", (counters or {}).get("decoder")),
-            "flops_per_step": flops, "bf16_activations": out["bf16"], "split_detail": out["split"]}
+            "flops_per_step": flops, "fp16_activations": out["fp16"], "bf16_activations": out["bf16"],
+            "split_detail": out["split"]}
 
 
 # ---------------------------------------------------------- CPU baseline --
@@ -560,7 +562,7 @@ def pmc_pass(workload: str) -> None:
         block, x = workloads.decoder_inputs()
         block, xg = block.cuda(), x.cuda()
         for _ in range(2):
-            nki_forward(block, xg, compute_dtype="split")
+            nki_forward(block, xg, compute_dtype="float16")
     else:
         raise SystemExit(f"unknown counter workload {workload!r}; one of {sorted(PMC_WORKLOADS)}")
     torch.cuda.synchronize()
@@ -748,8 +750,9 @@ def main() -> int:
             "roofline": roofline("mfma", r["tflops"], "TFLOP/s", ctr.get(f"attention_{H}x{S}"))}
     log("decoder block ...")
     dec = bench_decoder(max(3, args.steps // 10), 2, ctr)
-    log(f"  split {dec['us']:.1f} us ({dec['rel_err_vs_fp32_block']:.2e} vs fp32 block); "
-        f"bf16 {dec['bf16_activations']['us']:.1f} us ({dec['bf16_activations']['rel_err_vs_fp32_block']:.2e})")
+    log(f"  fp16 {dec['us']:.1f} us ({dec['rel_err_vs_fp32_block']:.2e} vs fp32 block); "
+        f"bf16 {dec['bf16_activations']['us']:.1f} us ({dec['bf16_activations']['rel_err_vs_fp32_block']:.2e}); "
+        f"split {dec['split_detail']['us']:.1f} us ({dec['split_detail']['rel_err_vs_fp32_block']:.2e})")
 
     result = {
         "metric": METRIC, "value": round(att["tflops"], 3), "unit": "TFLOP/s", "n_gpus": 1,

@@ -11,7 +11,10 @@
  *     softmax, the naive attention) take a caller-provided workspace whose
  *     size is reported by the matching *_workspace_bytes() function.
  *   - Strides (ld*, *_sh, *_ss, batch strides) are in ELEMENTS, not bytes.
- *   - dtype codes: NKL_F32 = 0 (float32), NKL_BF16 = 1 (bfloat16).
+ *   - dtype codes: NKL_F32 = 0 (float32), NKL_BF16 = 1 (bfloat16),
+ *     NKL_F16 = 2 (float16: the 16-bit operand format with 11 significant
+ *     bits, taken by the GEMMs, the RMSNorm output, the gate/up SwiGLU GEMM
+ *     and the causal attention; see each entry point).
  *   - `stream` is a hipStream_t passed as void* (0 = the null stream).  Every
  *     call only enqueues work and returns; it is asynchronous with respect to
  *     the host and re-entrant (no global state besides the per-thread error
@@ -30,7 +33,7 @@ extern "C" {
 
 #define NKL_ABI_VERSION 1
 
-enum { NKL_F32 = 0, NKL_BF16 = 1 };
+enum { NKL_F32 = 0, NKL_BF16 = 1, NKL_F16 = 2 };
 
 enum {
   NKL_OK = 0,
@@ -63,7 +66,10 @@ const char* nkl_last_error_string(void);
  *   R: optional residual added in the fp32 epilogue ([M, N], ldr, dtype_out);
  *      NULL for none.
  * Products accumulate in fp32; C is rounded once (round-to-nearest-even) to
- * dtype_out.  dtype_in in {F32, BF16}; dtype_out in {F32, dtype_in}.
+ * dtype_out.  dtype_in in {F32, BF16, F16}; dtype_out in {F32, dtype_in}.
+ * F16 operands take the LDS-DMA kernel only: 16-byte aligned A and B, K,
+ * lda, ldb (and N when b_trans == 0) multiples of 8, operands under 2 GiB;
+ * other F16 shapes return NKL_EDTYPE.
  */
 int nkl_gemm(const void* A, const void* B, void* C, const void* R,
              int M, int N, int K, long lda, long ldb, long ldc, long ldr,
@@ -76,15 +82,15 @@ int nkl_gemm(const void* A, const void* B, void* C, const void* R,
  * the SwiGLU between them in one GEMM (the fusion docs/STUDY_GUIDE.md:57
  * suggests for nkilab/model.py:88, which calls ops.swiglu, nkilab/ops.py:64,
  * on two matmul outputs).
- *   A:   [M, K] bf16 (lda >= K).
- *   Bgu: [2N, K] bf16 (ldb >= K), the rows of Wg and Wu ([N, K] each)
+ *   A:   [M, K] dtype (lda >= K), dtype in {BF16, F16}.
+ *   Bgu: [2N, K] dtype (ldb >= K), the rows of Wg and Wu ([N, K] each)
  *        interleaved in groups of 32: rows 64 j .. 64 j + 31 are Wg rows
  *        32 j .., rows 64 j + 32 .. 64 j + 63 are Wu rows 32 j ...
- *   C:   [M, N] bf16 (ldc >= N).
+ *   C:   [M, N] dtype (ldc >= N).
  * N must be a multiple of 32; pointers 16-byte aligned; K, lda, ldb, ldc
- * multiples of 8.  The gate and up accumulators are rounded to bf16 before
+ * multiples of 8.  The gate and up accumulators are rounded to dtype before
  * silu(gate) * up is formed in fp32 and rounded once, so C equals what two
- * bf16 GEMMs followed by nkl_swiglu produce.
+ * dtype GEMMs followed by a SwiGLU in dtype produce.
  */
 int nkl_gemm_swiglu(const void* A, const void* Bgu, void* C, int M, int N,
                     int K, long lda, long ldb, long ldc, int dtype,
@@ -122,8 +128,8 @@ int nkl_softmax_unfused(const void* x, void* y, void* workspace,
  * y = x * rsqrt(mean(x^2) + eps) * w.
  * Replaces nkilab/kernels/norm.py:92 (rmsnorm_fused), nkilab/ops.py:61.
  * x: [rows, cols] (ldx, dtype_in); w: [cols] (dtype_in); y: (ldy, dtype_out).
- * dtype_out in {dtype_in, BF16}: an fp32 residual stream can be normalised
- * straight into a bf16 GEMM operand.
+ * dtype_out in {dtype_in, BF16, F16 (dtype_in F32 only)}: an fp32 residual
+ * stream can be normalised straight into a 16-bit GEMM operand.
  */
 int nkl_rmsnorm(const void* x, const void* w, void* y, int rows, int cols,
                 long ldx, long ldy, float eps, int dtype_in, int dtype_out,
@@ -180,7 +186,8 @@ int nkl_stream_copy(const void* x, void* y, long nbytes, void* stream);
  * q, k, v, o: [H, S, d] with element strides (*_sh between heads, *_ss between
  * positions) and unit stride along d; any S >= 1, 1 <= d <= 128.
  * bf16: P is rounded to bf16 before P.V, statistics and O accumulate in fp32,
- * O is rounded once.  f32: everything in fp32.
+ * O is rounded once.  f16: the same with fp16 operands, P and O (the teams
+ * kernel for every shape).  f32: everything in fp32.
  */
 int nkl_flash_attn_causal(const void* q, const void* k, const void* v,
                           void* o, int H, int S, int d, long q_sh, long q_ss,

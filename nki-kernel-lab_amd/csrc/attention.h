@@ -14,14 +14,15 @@ struct AttnArgs {
   long q_sh, q_ss, k_sh, k_ss, v_sh, v_ss, o_sh, o_ss;
   float c;    // softmax scale * log2(e): p = exp2(s * c - m)
   int group;  // query heads per K/V head (grouped-query attention; 1 for multi-head)
+  int f16;    // 16-bit kernels: 1 for fp16 q, k, v, o (P rounded to fp16), 0 for bf16
 };
 
-// bf16 flash attention (flash_bf16.hip).  With a workspace of
+// bf16 (and fp16: AttnArgs::f16) flash attention (flash_bf16.hip).  With a workspace of
 // flash_bf16_workspace_bytes() bytes for partial states and a zeroed counter
 // array of flash_bf16_counter_bytes() bytes (left zero by every call), the
 // work is balanced over one workgroup per CU (stream-K); without them, each
 // workgroup takes one whole query block.
-size_t flash_bf16_workspace_bytes(int H, int S, int d);
+size_t flash_bf16_workspace_bytes(int H, int S, int d, bool f16 = false);
 size_t flash_bf16_counter_bytes(int H, int S);
 int flash_bf16_launch(const AttnArgs& a, void* workspace, size_t workspace_bytes, int* counters,
                       size_t counter_bytes, hipStream_t st);

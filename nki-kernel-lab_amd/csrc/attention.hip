@@ -336,7 +336,8 @@ static int check_attn(const char* fn, const void* q, const void* k, const void* 
                       int d, int dtype, const long* strides) {
   if (H < 0 || S < 0) return set_error(NKL_EINVAL, "%s: negative shape H=%d S=%d", fn, H, S);
   if (d < 1 || d > 128) return set_error(NKL_EINVAL, "%s: head dim d=%d outside [1, 128]", fn, d);
-  if (dtype != NKL_F32 && dtype != NKL_BF16) return set_error(NKL_EDTYPE, "%s: unsupported dtype %d", fn, dtype);
+  if (dtype != NKL_F32 && dtype != NKL_BF16 && dtype != NKL_F16)
+    return set_error(NKL_EDTYPE, "%s: unsupported dtype %d", fn, dtype);
   const int E = dtype == NKL_F32 ? 4 : 8;
   if (d % E != 0)
     return set_error(NKL_EINVAL, "%s: d=%d must be a multiple of %d (pad the head dim on the host)", fn, d, E);
@@ -360,12 +361,13 @@ static int flash_entry(const char* fn, const void* q, const void* k, const void*
     return set_error(NKL_EINVAL, "%s: H=%d query heads do not divide into Hkv=%d K/V heads", fn, H, Hkv);
   if (H == 0 || S == 0) return NKL_OK;
   AttnArgs a{q, k, v, o, H, S, d, st8[0], st8[1], st8[2], st8[3], st8[4], st8[5], st8[6], st8[7], scale * kLog2e,
-             H / Hkv};
+             H / Hkv, dtype == NKL_F16 ? 1 : 0};
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == NKL_BF16) {
+  if (dtype == NKL_BF16 || dtype == NKL_F16) {
     if (!ws_entry) return flash_bf16_launch(a, nullptr, 0, nullptr, 0, st);
     // Shapes that need no scratch (size 0) accept a null workspace.
-    if (!workspace && flash_bf16_workspace_bytes(H, S, d) > 0) return set_error(NKL_EWORKSPACE, "%s: null workspace", fn);
+    if (!workspace && flash_bf16_workspace_bytes(H, S, d, dtype == NKL_F16) > 0)
+      return set_error(NKL_EWORKSPACE, "%s: null workspace", fn);
     return flash_bf16_launch(a, workspace, workspace_bytes, counters, counter_bytes, st);
   }
   return flash_f32_dispatch(a, st);
@@ -380,12 +382,12 @@ extern "C" int nkl_flash_attn_causal(const void* q, const void* k, const void* v
 }
 
 extern "C" size_t nkl_flash_attn_causal_workspace_bytes(int H, int S, int d, int dtype) {
-  if (dtype != NKL_BF16) return 0;
-  return flash_bf16_workspace_bytes(H, S, d);
+  if (dtype != NKL_BF16 && dtype != NKL_F16) return 0;
+  return flash_bf16_workspace_bytes(H, S, d, dtype == NKL_F16);
 }
 
 extern "C" size_t nkl_flash_attn_causal_counter_bytes(int H, int S, int dtype) {
-  if (dtype != NKL_BF16) return 0;
+  if (dtype != NKL_BF16 && dtype != NKL_F16) return 0;
   return flash_bf16_counter_bytes(H, S);
 }
 
@@ -447,9 +449,9 @@ extern "C" int nkl_flash_attn_causal_noalloc(const void* q, const void* k, const
   const long strides[8] = {q_sh, q_ss, k_sh, k_ss, v_sh, v_ss, o_sh, o_ss};
   int rc = check_attn(fn, q, k, v, o, H, S, d, dtype, strides);
   if (rc) return rc;
-  if (dtype != NKL_BF16 || H == 0 || S == 0)  // no scratch on these paths
+  if ((dtype != NKL_BF16 && dtype != NKL_F16) || H == 0 || S == 0)  // no scratch on these paths
     return flash_entry(fn, q, k, v, o, nullptr, 0, nullptr, 0, true, H, Hkv, S, d, strides, scale, dtype, stream);
-  const size_t need = flash_bf16_workspace_bytes(H, S, d);
+  const size_t need = flash_bf16_workspace_bytes(H, S, d, dtype == NKL_F16);
   // One counter per 64-query block (the smallest block) covers every schedule.
   const size_t need_c = need ? (size_t)H * ((S + 63) / 64) * 4 : 0;
   if (need > kNoAllocPartBytes || need_c > kNoAllocCounterBytes)
@@ -486,6 +488,7 @@ extern "C" size_t nkl_attention_naive_workspace_bytes(int H, int S, int dtype) {
 static int naive_entry(const char* fn, const void* q, const void* k, const void* v, void* o, void* workspace,
                        size_t workspace_bytes, int H, int Hkv, int S, int d, const long* st8, float scale, int dtype,
                        void* stream) {
+  if (dtype == NKL_F16) return set_error(NKL_EDTYPE, "%s: the naive attention takes fp32 or bf16", fn);
   int rc = check_attn(fn, q, k, v, o, H, S, d, dtype, st8);
   if (rc) return rc;
   if (Hkv < 1 || H % Hkv != 0)

@@ -14,6 +14,9 @@ typedef __bf16 bf16;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16;
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
@@ -28,6 +31,8 @@ template <>
 __device__ __forceinline__ float to_f32<float>(float v) { return v; }
 template <>
 __device__ __forceinline__ float to_f32<bf16>(bf16 v) { return (float)v; }
+template <>
+__device__ __forceinline__ float to_f32<f16>(f16 v) { return (float)v; }
 
 // fp32 -> T, round-to-nearest-even (v_cvt_pk_bf16_f32 on gfx950).
 template <typename T>
@@ -36,11 +41,20 @@ template <>
 __device__ __forceinline__ float from_f32<float>(float v) { return v; }
 template <>
 __device__ __forceinline__ bf16 from_f32<bf16>(float v) { return (bf16)v; }
+template <>
+__device__ __forceinline__ f16 from_f32<f16>(float v) { return (f16)v; }
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   bf16x2 r;
   r[0] = (bf16)lo;
   r[1] = (bf16)hi;
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  f16x2 r;
+  r[0] = (f16)lo;
+  r[1] = (f16)hi;
   return __builtin_bit_cast(uint32_t, r);
 }
 
@@ -81,6 +95,12 @@ __device__ __forceinline__ void load16(const bf16* p, float (&v)[8]) {
   v[6] = bf16lo(t.w); v[7] = bf16hi(t.w);
 }
 
+__device__ __forceinline__ void load16(const f16* p, float (&v)[8]) {
+  const f16x8 t = *reinterpret_cast<const f16x8*>(p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = (float)t[i];
+}
+
 // Store E fp32 values as E elements of T (E * sizeof(T) bytes, aligned).
 template <int E>
 __device__ __forceinline__ void store_vec(float* p, const float (&v)[E]) {
@@ -102,6 +122,24 @@ __device__ __forceinline__ void store_vec(bf16* p, const float (&v)[E]) {
     uint2 t;
     t.x = pack_bf16x2(v[0], v[1]);
     t.y = pack_bf16x2(v[2], v[3]);
+    *reinterpret_cast<uint2*>(p) = t;
+  }
+}
+
+template <int E>
+__device__ __forceinline__ void store_vec(f16* p, const float (&v)[E]) {
+  static_assert(E == 4 || E == 8, "fp16 vector store of 4 or 8 elements");
+  if constexpr (E == 8) {
+    uint4 t;
+    t.x = pack_f16x2(v[0], v[1]);
+    t.y = pack_f16x2(v[2], v[3]);
+    t.z = pack_f16x2(v[4], v[5]);
+    t.w = pack_f16x2(v[6], v[7]);
+    *reinterpret_cast<uint4*>(p) = t;
+  } else {
+    uint2 t;
+    t.x = pack_f16x2(v[0], v[1]);
+    t.y = pack_f16x2(v[2], v[3]);
     *reinterpret_cast<uint2*>(p) = t;
   }
 }
@@ -128,6 +166,20 @@ __device__ __forceinline__ void store_vec_nt(bf16* p, const float (&v)[E]) {
     __builtin_nontemporal_store(t, reinterpret_cast<u4*>(p));
   } else {
     const u2 t = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    __builtin_nontemporal_store(t, reinterpret_cast<u2*>(p));
+  }
+}
+
+template <int E>
+__device__ __forceinline__ void store_vec_nt(f16* p, const float (&v)[E]) {
+  static_assert(E == 4 || E == 8, "fp16 vector store of 4 or 8 elements");
+  typedef unsigned u4 __attribute__((ext_vector_type(4)));
+  typedef unsigned u2 __attribute__((ext_vector_type(2)));
+  if constexpr (E == 8) {
+    const u4 t = {pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3]), pack_f16x2(v[4], v[5]), pack_f16x2(v[6], v[7])};
+    __builtin_nontemporal_store(t, reinterpret_cast<u4*>(p));
+  } else {
+    const u2 t = {pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])};
     __builtin_nontemporal_store(t, reinterpret_cast<u2*>(p));
   }
 }
@@ -192,6 +244,28 @@ struct Mfma32<float> {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
   }
 };
+
+// A 32x32x16 MFMA on 16-bit operands held as 16-byte vectors (the bf16x8
+// register type carries either format's bits): fp16 when H, else bf16.  The
+// kernels that take both formats move operands as raw 16-bit values and only
+// pick the instruction (and the rounding of what they produce) by H.
+template <bool H>
+__device__ __forceinline__ floatx16 mma32_16b(bf16x8 a, bf16x8 b, floatx16 c) {
+  if constexpr (H)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                   0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+// fp32 -> the 16-bit format (round to nearest even), as a bf16-typed value
+// holding its bits.
+template <bool H>
+__device__ __forceinline__ bf16 round16(float x) {
+  if constexpr (H)
+    return __builtin_bit_cast(bf16, (f16)x);
+  else
+    return (bf16)x;
+}
 
 // 16-byte load of base[off] when `ok`, zeros otherwise.  The load itself is
 // unconditional (from base[0] when !ok) so that the compiler never turns the

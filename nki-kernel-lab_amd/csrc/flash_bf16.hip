@@ -90,13 +90,14 @@ __device__ __forceinline__ bf16x8 read_vt_frag(const bf16* row_a, const bf16* ro
 
 }  // namespace
 
-template <int D, int WPT, int NT>
+template <int D, int WPT, int NT, bool H = false>
 // Two wavefronts per SIMD (at most 256 registers each): a 4-wavefront
-// workgroup then shares its CU with a second one.
+// workgroup then shares its CU with a second one.  H: fp16 operands, P and O
+// (the 16-bit values move as raw bits; only the MFMA and the roundings of P
+// and O depend on the format).
 __global__ __launch_bounds__(64 * WPT * NT) __attribute__((amdgpu_waves_per_eu(2)))
 void flash_bf16_kernel(AttnArgs p, Work w) {
   using L = Layout<D, WPT, NT>;
-  using MF = Mfma32<bf16>;
   constexpr int QB = L::QB, TT = L::TT;
   constexpr int CPR = D / 8;                    // 16-byte chunks per K/V row
   constexpr int NCHUNK = BN * CPR;              // chunks per K (or V) tile
@@ -239,7 +240,7 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
 #pragma unroll
       for (int uu = 0; uu < 2; ++uu)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) pf[uu][j] = (bf16)sc[8 * uu + j];
+        for (int j = 0; j < 8; ++j) pf[uu][j] = round16<H>(sc[8 * uu + j]);
     };
     // O += P V for the tile in stage sb.  The V^T fragments of two d-blocks
     // are read together before their MFMAs, so that the MFMAs wait on LDS
@@ -260,7 +261,7 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
-          for (int uu = 0; uu < 2; ++uu) oacc[d0 + g] = MF::mma(a[g][uu], pf[uu], oacc[d0 + g]);
+          for (int uu = 0; uu < 2; ++uu) oacc[d0 + g] = mma32_16b<H>(a[g][uu], pf[uu], oacc[d0 + g]);
       }
     };
 
@@ -289,7 +290,7 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
           for (int f = 0; f < NQF; ++f) kf[f] = load_frag(sb + kfrag_off + 16 * f);
           __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int f = 0; f < NQF; ++f) sacc = MF::mma(kf[f], qf[f], sacc);
+          for (int f = 0; f < NQF; ++f) sacc = mma32_16b<H>(kf[f], qf[f], sacc);
           __builtin_amdgcn_sched_barrier(0);
         }
         lstore((it + 1) & 1, rk, rv);
@@ -436,7 +437,7 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
         for (int bq = 0; bq < 4; ++bq) {
           bf16x4 v4;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v4[e] = (bf16)(own[j][4 * bq + e] * linv);
+          for (int e = 0; e < 4; ++e) v4[e] = round16<H>(own[j][4 * bq + e] * linv);
           *reinterpret_cast<bf16x4*>(stg + l32 * PITCH + 32 * j + 8 * bq + 4 * h32) = v4;
         }
       bf16* obase = static_cast<bf16*>(p.o) + (long)hh * p.o_sh + 32 * own0;
@@ -1207,7 +1208,7 @@ Work plan(int H, int S, Config cfg) {
 // needs no partial states.
 // The overrides above replace the choice (tests, tuning); the
 // one-wavefront-per-SIMD kernels and kFwd take 64 < d <= 128 and fix the block.
-Config choose(int H, int S, int d) {
+Config choose(int H, int S, int d, bool f16) {
   const long cus = cu_count();
   const long nqb = (S + 127) / 128;
   const long units128 = (long)H * (2 * (nqb - 1) * nqb + (S - 1) / BN + 1);
@@ -1220,6 +1221,7 @@ Config choose(int H, int S, int d) {
   if (ov.qb >= 0) cfg.qb = ov.qb;
   if (ov.kern >= 0) cfg.kern = ov.kern;
   if (d <= 64 && cfg.kern != kTeams4) cfg.kern = kTeams;
+  if (f16 && cfg.kern != kTeams4) cfg.kern = kTeams;  // fp16: the teams kernels only
   if (cfg.kern == kW32x4 || cfg.kern == kW64x2 || cfg.kern == kW32x4x2 || cfg.kern == kFwd || cfg.kern == kFwdPP)
     cfg.qb = 128;
   if (cfg.kern == kW64x4) cfg.qb = 256;
@@ -1241,7 +1243,10 @@ size_t part_floats_for(int d, const Config& cfg) {
 
 template <int D, int WPT, int NT>
 void launch(const AttnArgs& a, const Work& w, hipStream_t st) {
-  flash_bf16_kernel<D, WPT, NT><<<dim3((unsigned)w.grid), dim3(64 * WPT * NT), 0, st>>>(a, w);
+  if (a.f16)
+    flash_bf16_kernel<D, WPT, NT, true><<<dim3((unsigned)w.grid), dim3(64 * WPT * NT), 0, st>>>(a, w);
+  else
+    flash_bf16_kernel<D, WPT, NT, false><<<dim3((unsigned)w.grid), dim3(64 * WPT * NT), 0, st>>>(a, w);
 }
 
 template <int QH, int NW, int OCC = 1>
@@ -1265,9 +1270,9 @@ void launch_qb(const AttnArgs& a, const Work& w, int qb, int kern, hipStream_t s
 
 }  // namespace
 
-size_t flash_bf16_workspace_bytes(int H, int S, int d) {
+size_t flash_bf16_workspace_bytes(int H, int S, int d, bool f16) {
   if (H <= 0 || S <= 0) return 0;
-  const Config cfg = choose(H, S, d);
+  const Config cfg = choose(H, S, d, f16);
   if (cfg.sched != kBalanced) return 0;
   return (size_t)plan(H, S, cfg).grid * 2 * part_floats_for(d, cfg) * 4;
 }
@@ -1276,17 +1281,17 @@ size_t flash_bf16_workspace_bytes(int H, int S, int d) {
 // block) whenever some head dim takes the balanced schedule for this shape.
 size_t flash_bf16_counter_bytes(int H, int S) {
   if (H <= 0 || S <= 0) return 0;
-  if (choose(H, S, 32).sched != kBalanced && choose(H, S, 128).sched != kBalanced) return 0;
+  if (choose(H, S, 32, false).sched != kBalanced && choose(H, S, 128, false).sched != kBalanced) return 0;
   return (size_t)H * ((S + 63) / 64) * 4;
 }
 
 int flash_bf16_launch(const AttnArgs& a, void* workspace, size_t workspace_bytes, int* counters,
                       size_t counter_bytes, hipStream_t st) {
-  Config cfg = choose(a.H, a.S, a.d);
+  Config cfg = choose(a.H, a.S, a.d, a.f16 != 0);
   if (cfg.sched == kBalanced && !workspace) cfg.sched = kPairs;  // the plain entry point: no scratch
   Work w = plan(a.H, a.S, cfg);
   if (cfg.sched == kBalanced) {
-    const size_t need = flash_bf16_workspace_bytes(a.H, a.S, a.d);
+    const size_t need = flash_bf16_workspace_bytes(a.H, a.S, a.d, a.f16 != 0);
     const size_t need_c = (size_t)a.H * w.nqb * 4;
     if (workspace_bytes < need || !counters || counter_bytes < need_c)
       return set_error(NKL_EWORKSPACE,

@@ -296,9 +296,12 @@ constexpr unsigned kOOB = 0x80000000u;  // a buffer offset past every range: the
 
 }  // namespace
 
-template <typename TO, int BM, int BN, bool BT, int NS, int WGM = 2, int WGN = 2>
+template <typename TI, typename TO, int BM, int BN, bool BT, int NS, int WGM = 2, int WGN = 2>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_dma_kernel(GemmArgs p) {
-  using MF = Mfma32<bf16>;
+  // TI: the 16-bit operand format (bf16 or fp16); operands move as raw 16-bit
+  // values, the format only picks the MFMA.
+  constexpr bool H = std::is_same<TI, f16>::value;
+  static_assert(H || std::is_same<TI, bf16>::value, "16-bit operands");
   constexpr int NW = WGM * WGN;
   constexpr int A_BYTES = BM * 128;
   constexpr int B_BYTES = BN * 128;  // BN rows of 128 B (B^T) or BN / 64 sub-tiles of 64 x 128 B
@@ -458,7 +461,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_dma_kernel(GemmArgs p) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = MF::mma(af[i], bfr[j], acc[i][j]);
+      for (int j = 0; j < TN; ++j) acc[i][j] = mma32_16b<H>(af[i], bfr[j], acc[i][j]);
   };
   // Every wavefront's copies of a stage have landed once each waited for its
   // own (vmcnt) and all passed the barrier.  A bare s_barrier, not
@@ -496,7 +499,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_dma_kernel(GemmArgs p) {
     const int per = (u1 - u0 + NMMA - 1) / NMMA;
 #pragma unroll
     for (int k = 0; k < NMMA; ++k) {
-      acc[k / TN][k % TN] = MF::mma(af[k / TN], bfr[k % TN], acc[k / TN][k % TN]);
+      acc[k / TN][k % TN] = mma32_16b<H>(af[k / TN], bfr[k % TN], acc[k / TN][k % TN]);
 #pragma unroll
       for (int u = u0 + k * per; u < u0 + (k + 1) * per && u < u1; ++u) dma1(sd, sd % NS, u);
       __builtin_amdgcn_sched_barrier(0);
@@ -553,7 +556,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_dma_kernel(GemmArgs p) {
     // passes.  With the SwiGLU pairing, tiles 2k and 2k+1 of the wavefront
     // hold gate and up for the same 32 output columns (the weight rows are
     // interleaved in groups of 32), and the block written is
-    // silu(bf16(gate)) * bf16(up): the values a gate and an up GEMM with bf16
+    // silu(TO(gate)) * TO(up): the values a gate and an up GEMM with TO
     // outputs would hand the SwiGLU kernel.
     constexpr int OE = 16 / sizeof(TO);  // output elements per 16-byte store
     constexpr int WC_MAX = WN;           // staged columns per wavefront (SwiGLU: WN / 2)
@@ -579,8 +582,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_dma_kernel(GemmArgs p) {
             for (int k = 0; k < TN / 2; ++k)
 #pragma unroll
               for (int e = 0; e < 16; ++e) {
-                const float g = to_f32<bf16>((bf16)acc[ip * TP + t][2 * k][e]);
-                const float u = to_f32<bf16>((bf16)acc[ip * TP + t][2 * k + 1][e]);
+                const float g = to_f32<TO>(from_f32<TO>(acc[ip * TP + t][2 * k][e]));
+                const float u = to_f32<TO>(from_f32<TO>(acc[ip * TP + t][2 * k + 1][e]));
                 stg[(t * 32 + 8 * (e / 4) + 4 * lg + (e % 4)) * PITCH + k * 32 + lr] = silu(g) * u;
               }
         }
@@ -652,19 +655,19 @@ static bool staged_ok(const GemmArgs& a) {
 // Tiles of the LDS-DMA kernel.
 enum DmaTile { kT64x64, kT64x128, kT128x128, kT128x256, kT256x128, kT256x192, kT256x256, kTileCount };
 
-template <typename TO, bool BT>
+template <typename TI, typename TO, bool BT>
 static void launch_dma(DmaTile t, const GemmArgs& g, int batch, hipStream_t st) {
   auto grid = [&](int bm, int bn) {
     return dim3((unsigned)((long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn)), 1, (unsigned)batch);
   };
   switch (t) {
-    case kT256x256: gemm_dma_kernel<TO, 256, 256, BT, 2, 2, 4><<<grid(256, 256), dim3(512), 0, st>>>(g); break;
-    case kT256x192: gemm_dma_kernel<TO, 256, 192, BT, 2, 4, 2><<<grid(256, 192), dim3(512), 0, st>>>(g); break;
-    case kT256x128: gemm_dma_kernel<TO, 256, 128, BT, 3, 4, 2><<<grid(256, 128), dim3(512), 0, st>>>(g); break;
-    case kT128x256: gemm_dma_kernel<TO, 128, 256, BT, 3, 2, 4><<<grid(128, 256), dim3(512), 0, st>>>(g); break;
-    case kT128x128: gemm_dma_kernel<TO, 128, 128, BT, 4><<<grid(128, 128), dim3(256), 0, st>>>(g); break;
-    case kT64x128: gemm_dma_kernel<TO, 64, 128, BT, 6><<<grid(64, 128), dim3(256), 0, st>>>(g); break;
-    default: gemm_dma_kernel<TO, 64, 64, BT, 8><<<grid(64, 64), dim3(256), 0, st>>>(g); break;
+    case kT256x256: gemm_dma_kernel<TI, TO, 256, 256, BT, 2, 2, 4><<<grid(256, 256), dim3(512), 0, st>>>(g); break;
+    case kT256x192: gemm_dma_kernel<TI, TO, 256, 192, BT, 2, 4, 2><<<grid(256, 192), dim3(512), 0, st>>>(g); break;
+    case kT256x128: gemm_dma_kernel<TI, TO, 256, 128, BT, 3, 4, 2><<<grid(256, 128), dim3(512), 0, st>>>(g); break;
+    case kT128x256: gemm_dma_kernel<TI, TO, 128, 256, BT, 3, 2, 4><<<grid(128, 256), dim3(512), 0, st>>>(g); break;
+    case kT128x128: gemm_dma_kernel<TI, TO, 128, 128, BT, 4><<<grid(128, 128), dim3(256), 0, st>>>(g); break;
+    case kT64x128: gemm_dma_kernel<TI, TO, 64, 128, BT, 6><<<grid(64, 128), dim3(256), 0, st>>>(g); break;
+    default: gemm_dma_kernel<TI, TO, 64, 64, BT, 8><<<grid(64, 64), dim3(256), 0, st>>>(g); break;
   }
 }
 
@@ -717,6 +720,19 @@ static int gemm_dispatch(const GemmArgs& a, int batch, int variant, hipStream_t 
   constexpr int E = VecE<T>::value;
   const bool vec = aligned16(a.A) && aligned16(a.B) && a.K % E == 0 && a.lda % E == 0 && a.ldb % E == 0 &&
                    a.sA % E == 0 && a.sB % E == 0 && (BT || a.N % E == 0);
+  constexpr bool half = std::is_same<T, f16>::value;
+  if constexpr (half) {
+    // fp16 operands: the LDS-DMA kernel only.
+    const long a_bytes = 2L * ((long)(a.M - 1) * a.lda + a.K), b_bytes = BT ? 2L * ((long)(a.N - 1) * a.ldb + a.K)
+                                                                        : 2L * ((long)(a.K - 1) * a.ldb + a.N);
+    if (variant == NKL_GEMM_NAIVE || !vec || a_bytes >= (1L << 31) || b_bytes >= (1L << 31))
+      return set_error(NKL_EDTYPE, "nkl_gemm: fp16 operands need the blocked variant, 16-byte aligned operands with K "
+                       "and leading dimensions multiples of 8, and operands under 2 GiB");
+    GemmArgs g = a;
+    g.epi = staged_ok<TO>(a) ? kEpiStaged : kEpiElem;
+    launch_dma<f16, TO, BT>(choose_tile(a, batch), g, batch, st);
+    return check_launch("nkl_gemm(blocked)");
+  } else {
   if (variant == NKL_GEMM_NAIVE || !vec) {
     const long tiles = (long)((a.M + 31) / 32) * ((a.N + 31) / 32);
     gemm_naive_kernel<T, TO, BT><<<dim3((unsigned)((tiles + 3) / 4), 1, batch), dim3(256), 0, st>>>(a);
@@ -731,7 +747,7 @@ static int gemm_dispatch(const GemmArgs& a, int batch, int variant, hipStream_t 
     if (a_bytes < (1L << 31) && b_bytes < (1L << 31)) {
       GemmArgs g = a;
       g.epi = staged_ok<TO>(a) ? kEpiStaged : kEpiElem;
-      launch_dma<TO, BT>(choose_tile(a, batch), g, batch, st);
+      launch_dma<bf16, TO, BT>(choose_tile(a, batch), g, batch, st);
       return check_launch("nkl_gemm(blocked)");
     }
   }
@@ -746,6 +762,7 @@ static int gemm_dispatch(const GemmArgs& a, int batch, int variant, hipStream_t 
     gemm_blocked_kernel<T, TO, 64, 64, BT><<<dim3((unsigned)tiles, 1, batch), dim3(256), 0, st>>>(a);
   }
   return check_launch("nkl_gemm(blocked)");
+  }
 }
 
 template <typename T, typename TO>
@@ -774,6 +791,8 @@ extern "C" int nkl_gemm(const void* A, const void* B, void* C, const void* R, in
   if (dtype_in == NKL_F32 && dtype_out == NKL_F32) return gemm_layout<float, float>(a, b_trans, batch, variant, st);
   if (dtype_in == NKL_BF16 && dtype_out == NKL_BF16) return gemm_layout<bf16, bf16>(a, b_trans, batch, variant, st);
   if (dtype_in == NKL_BF16 && dtype_out == NKL_F32) return gemm_layout<bf16, float>(a, b_trans, batch, variant, st);
+  if (dtype_in == NKL_F16 && dtype_out == NKL_F16) return gemm_layout<f16, f16>(a, b_trans, batch, variant, st);
+  if (dtype_in == NKL_F16 && dtype_out == NKL_F32) return gemm_layout<f16, float>(a, b_trans, batch, variant, st);
   return set_error(NKL_EDTYPE, "nkl_gemm: unsupported dtype pair (%d -> %d)", dtype_in, dtype_out);
 }
 
@@ -781,7 +800,8 @@ extern "C" int nkl_gemm_swiglu(const void* A, const void* Bgu, void* C, int M, i
                                long ldc, int dtype, void* stream) {
   if (M < 0 || N < 0 || K < 0)
     return set_error(NKL_EINVAL, "nkl_gemm_swiglu: negative shape M=%d N=%d K=%d", M, N, K);
-  if (dtype != NKL_BF16) return set_error(NKL_EDTYPE, "nkl_gemm_swiglu: only bf16 is supported (dtype %d)", dtype);
+  if (dtype != NKL_BF16 && dtype != NKL_F16)
+    return set_error(NKL_EDTYPE, "nkl_gemm_swiglu: only bf16 and fp16 are supported (dtype %d)", dtype);
   if (M == 0 || N == 0) return NKL_OK;
   if (N % 32 != 0) return set_error(NKL_EINVAL, "nkl_gemm_swiglu: N=%d must be a multiple of 32", N);
   if (!A || !Bgu || !C) return set_error(NKL_EINVAL, "nkl_gemm_swiglu: null operand pointer");
@@ -801,7 +821,10 @@ extern "C" int nkl_gemm_swiglu(const void* A, const void* Bgu, void* C, int M, i
   DmaTile t = choose_tile(a, 1);
   if (t == kT64x64) t = kT64x128;
   if (t == kT256x192) t = kT256x256;
-  launch_dma<bf16, true>(t, a, 1, st);
+  if (dtype == NKL_F16)
+    launch_dma<f16, f16, true>(t, a, 1, st);
+  else
+    launch_dma<bf16, bf16, true>(t, a, 1, st);
   return check_launch("nkl_gemm_swiglu");
 }
 

@@ -470,6 +470,9 @@ extern "C" int nkl_rmsnorm_ex(const void* x, const void* w, void* y, int rows, i
   if (dtype_in == NKL_F32 && dtype_out == NKL_BF16)
     return wf ? rmsnorm_launch<float, float, bf16>(x, w, y, rows, cols, ldx, ldy, eps, st)
               : rmsnorm_launch<float, bf16, bf16>(x, w, y, rows, cols, ldx, ldy, eps, st);
+  if (dtype_in == NKL_F32 && dtype_out == NKL_F16)
+    return wf ? rmsnorm_launch<float, float, f16>(x, w, y, rows, cols, ldx, ldy, eps, st)
+              : rmsnorm_launch<float, bf16, f16>(x, w, y, rows, cols, ldx, ldy, eps, st);
   return set_error(NKL_EDTYPE, "nkl_rmsnorm: unsupported dtype pair (%d -> %d)", dtype_in, dtype_out);
 }
 

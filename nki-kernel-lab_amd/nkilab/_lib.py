@@ -11,7 +11,7 @@ import os
 LIB_NAME = "libnkilab_hip.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-F32, BF16 = 0, 1
+F32, BF16, F16 = 0, 1, 2
 GEMM_BLOCKED, GEMM_NAIVE = 0, 1
 ABI_VERSION = 1
 

@@ -29,11 +29,15 @@ def device() -> torch.device:
 
 
 def dtype_code(dt: torch.dtype) -> int:
+    """The C ABI's dtype code (float16 is an operand format of the GEMM, the
+    RMSNorm output, the gate/up SwiGLU GEMM and the flash attention only)."""
     if dt == torch.float32:
         return _lib.F32
     if dt == torch.bfloat16:
         return _lib.BF16
-    raise TypeError(f"unsupported dtype {dt}: float32 or bfloat16 expected")
+    if dt == torch.float16:
+        return _lib.F16
+    raise TypeError(f"unsupported dtype {dt}: float32, bfloat16 or float16 expected")
 
 
 def to_device(x) -> tuple[torch.Tensor, str]:

@@ -27,6 +27,11 @@ Differences from the reference's host glue, none of which changes the math:
   * ``compute_dtype="bfloat16"`` runs the block in bf16 with an fp32 residual
     stream (the GEMMs that feed the residual emit fp32).  The default keeps
     the reference's behaviour: everything in x's dtype.
+  * ``compute_dtype="float16"`` runs the same kernels with fp16 activations
+    and weights (fp32 x and residual stream): 11 significant bits per
+    rounding instead of bf16's 8, which keeps the block within 1e-3 of the
+    fp32 block at the bf16 path's cost (the activations must stay inside
+    fp16's range, |v| < 65504).
   * ``compute_dtype="split"`` keeps fp32 activations and the fp32 residual
     but runs the projections on bf16 MFMA: every GEMM operand is an fp32
     activation carried as a bf16 hi/lo pair (K doubled) against the bf16
@@ -128,8 +133,8 @@ class DecoderBlock(nn.Module):
         return x + self.wd(F.silu(self.wg(h)) * self.wu(h))
 
 
-_DTYPES = {"float32": torch.float32, "bfloat16": torch.bfloat16, torch.float32: torch.float32,
-           torch.bfloat16: torch.bfloat16}
+_DTYPES = {"float32": torch.float32, "bfloat16": torch.bfloat16, "float16": torch.float16,
+           torch.float32: torch.float32, torch.bfloat16: torch.bfloat16, torch.float16: torch.float16}
 SPLIT = "split"
 
 
@@ -146,16 +151,17 @@ def _device_param(block: nn.Module, name: str, p: torch.Tensor, dtype: torch.dty
     return t
 
 
-def _packed_gate_up(block: DecoderBlock, dev: torch.device) -> torch.Tensor:
-    """pack_gate_up(Wg, Wu) in bf16 on dev, rebuilt when either weight changes."""
+def _packed_gate_up(block: DecoderBlock, dev: torch.device, dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """pack_gate_up(Wg, Wu) in `dtype` (bf16 or fp16) on dev, rebuilt when
+    either weight changes."""
     cache = block.__dict__.setdefault("_nkl_param_cache", {})
-    key = ("gate_up", torch.bfloat16, dev)
+    key = ("gate_up", dtype, dev)
     stamp = tuple((p.data_ptr(), p._version) for p in (block.wg.weight, block.wu.weight))
     hit = cache.get(key)
     if hit is not None and hit[0] == stamp:
         return hit[1]
-    wg = block.wg.weight.detach().to(device=dev, dtype=torch.bfloat16)
-    wu = block.wu.weight.detach().to(device=dev, dtype=torch.bfloat16)
+    wg = block.wg.weight.detach().to(device=dev, dtype=dtype)
+    wu = block.wu.weight.detach().to(device=dev, dtype=dtype)
     t = ops.pack_gate_up(wg, wu)
     cache[key] = (stamp, t)
     return t
@@ -231,8 +237,9 @@ def nki_forward(block: DecoderBlock, x, attention_variant: str = "flash_pipeline
     x: [S, d_model] as NumPy or torch (CPU or GPU); returns the same kind.
     compute_dtype: None (= x's dtype, the reference's behaviour), "bfloat16"
     for bf16 GEMM/attention operands with the residual stream kept in x's
-    dtype, or "split" (fp32 x only) for fp32 activations with the projections
-    on bf16 MFMA over hi/lo operand pairs.
+    dtype, "float16" (fp32 x only) for fp16 operands (within 1e-3 of the fp32
+    block at bf16 cost), or "split" (fp32 x only) for fp32 activations with
+    the projections on bf16 MFMA over hi/lo operand pairs.
     """
     cfg = block.cfg
     xt, kind = to_device(x)
@@ -247,6 +254,8 @@ def nki_forward(block: DecoderBlock, x, attention_variant: str = "flash_pipeline
     cdt = rdt if compute_dtype is None else _DTYPES[compute_dtype]
     if cdt == torch.float32 and rdt == torch.bfloat16:
         raise ValueError("nki_forward: fp32 compute on a bf16 residual stream is not supported")
+    if cdt == torch.float16 and rdt != torch.float32:
+        raise ValueError("nki_forward: compute_dtype='float16' needs an fp32 x")
     W = {n: _device_param(block, n, getattr(block, n).weight, cdt, dev) for n in ("wqkv", "wo", "wg", "wu", "wd")}
     g1 = _device_param(block, "norm1", block.norm1.weight, rdt, dev)
     g2 = _device_param(block, "norm2", block.norm2.weight, rdt, dev)
@@ -270,9 +279,9 @@ def nki_forward(block: DecoderBlock, x, attention_variant: str = "flash_pipeline
     h2 = torch.empty((S, d), dtype=cdt, device=dev)
     ops.rmsnorm_into(x1, g2, h2, cfg.eps)
     act = torch.empty((S, cfg.d_ff), dtype=cdt, device=dev)
-    if cdt == torch.bfloat16 and cfg.d_ff % ops.GATE_UP_GROUP == 0 and d % 8 == 0:
+    if cdt in (torch.bfloat16, torch.float16) and cfg.d_ff % ops.GATE_UP_GROUP == 0 and d % 8 == 0:
         # gate, up and SwiGLU in one GEMM over the packed weight (same values)
-        ops.gemm_swiglu_into(h2, _packed_gate_up(block, dev), act)
+        ops.gemm_swiglu_into(h2, _packed_gate_up(block, dev, cdt), act)
     else:
         gate = torch.empty((S, cfg.d_ff), dtype=cdt, device=dev)
         up = torch.empty((S, cfg.d_ff), dtype=cdt, device=dev)

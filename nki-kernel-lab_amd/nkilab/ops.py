@@ -135,16 +135,17 @@ def pack_gate_up(wg: torch.Tensor, wu: torch.Tensor) -> torch.Tensor:
 
 def gemm_swiglu_into(a: torch.Tensor, w_gu: torch.Tensor, c: torch.Tensor) -> torch.Tensor:
     """c = silu(a @ Wg^T) * (a @ Wu^T) in one GEMM (model.py:88's gate, up and
-    SwiGLU), for bf16 a [M, K], the packed weight w_gu = pack_gate_up(Wg, Wu)
-    [2N, K] and c [M, N].  Equal to two bf16 linear_into calls and swiglu_into."""
+    SwiGLU), for bf16 (or fp16) a [M, K], the packed weight w_gu =
+    pack_gate_up(Wg, Wu) [2N, K] and c [M, N], all of one dtype.  Equal to two
+    linear_into calls in that dtype and a SwiGLU in that dtype."""
     M, K = a.shape
     N = c.shape[1]
     if c.shape[0] != M:
         raise ValueError(f"gemm_swiglu_into: output {tuple(c.shape)} does not have the {M} rows of a")
     if w_gu.shape != (2 * N, K):
         raise ValueError(f"gemm_swiglu_into: packed weight {tuple(w_gu.shape)} does not match [2*{N}, {K}]")
-    if not (a.dtype == w_gu.dtype == c.dtype == torch.bfloat16):
-        raise TypeError("gemm_swiglu_into: bf16 operands only")
+    if not (a.dtype == w_gu.dtype == c.dtype) or a.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError("gemm_swiglu_into: bf16 or fp16 operands, all of one dtype")
     a, lda = _row_major(a, K)
     wm, ldw = _row_major(w_gu, K)
     if c.dim() != 2 or (c.stride(1) != 1 and N > 1) or (M > 1 and c.stride(0) < N):
@@ -378,7 +379,7 @@ def attention_into(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.T
                          "and k, v share q's dtype")
     if scale is None:
         scale = 1.0 / math.sqrt(d)
-    E = 8 if q.dtype == torch.bfloat16 else 4
+    E = 8 if q.element_size() == 2 else 4
     q, k, v = (_attn_operand(t, E) for t in (q, k, v))
     o_ok = o.stride(2) == 1 and o.data_ptr() % 16 == 0 and o.stride(0) % E == 0 and o.stride(1) % E == 0
     out = o if o_ok else torch.empty((H, S, d), dtype=o.dtype, device=o.device)
@@ -438,7 +439,7 @@ def attention(q, k, v, variant: str = "flash_pipelined"):
                          f"{tuple(tq.shape)}, {tuple(tk.shape)}, {tuple(tv.shape)}")
     H, S, d = tq.shape
     assert d <= 128, "head dim must be <= 128"
-    E = 8 if tq.dtype == torch.bfloat16 else 4
+    E = 8 if tq.element_size() == 2 else 4
     dp = -(-d // E) * E
     if dp != d:
         tq, tk, tv = (torch.nn.functional.pad(t, (0, dp - d)) for t in (tq, tk, tv))
