@@ -491,8 +491,8 @@ def cpu_rows_baseline(ncores: int) -> dict:
 COUNTERS_FILE = os.path.join(ROOT, "profiles", "counters.json")
 COPY_BYTES = 256 << 20
 COUNTER_SETS = {"fetch": ["FETCH_SIZE"], "write": ["WRITE_SIZE"],
-                "mfma": ["SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CU_CYCLES",
-                         "GRBM_GUI_ACTIVE"]}
+                "mfma": ["SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_INSTS_VALU_MFMA_MOPS_F16", "SQ_VALU_MFMA_BUSY_CYCLES",
+                         "SQ_BUSY_CU_CYCLES", "GRBM_GUI_ACTIVE"]}
 # workload -> kernel-name substring of its dominant kernel ("" = every kernel
 # of the workload but the calibration copy)
 PMC_WORKLOADS = {"attention": "flash", "attention_1x4096": "flash", "attention_32x16384": "flash",
@@ -569,15 +569,17 @@ def pmc_pass(workload: str) -> None:
     log(f"pmc pass {workload} done")
 
 
-def collect_counters(out_dir: str) -> dict:
-    """Every counter pass of every workload under rocprofv3 (one child process
-    each, under `timeout -s KILL`), then profiles/counters.json from them."""
+def collect_counters(out_dir: str, only: list[str] | None = None) -> dict:
+    """Every counter pass of every workload (or of the workloads in `only`,
+    whose entries then replace those of the existing file) under rocprofv3
+    (one child process each, under `timeout -s KILL`), then
+    profiles/counters.json from them."""
     import glob
     import subprocess
 
     out_dir = os.path.abspath(out_dir)
     env = dict(os.environ, TMPDIR="/tmp")
-    for wl in PMC_WORKLOADS:
+    for wl in (only or PMC_WORKLOADS):
         for tag, ctrs in COUNTER_SETS.items():
             d = os.path.join(out_dir, f"{wl}_{tag}")
             cmd = ["timeout", "-s", "KILL", "180", "rocprofv3", "--pmc", *ctrs, "-d", d, "-o", "c", "-f", "csv", "--",
@@ -586,7 +588,7 @@ def collect_counters(out_dir: str) -> dict:
             r = subprocess.run(cmd, cwd="/tmp", env=env, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
             if r.returncode != 0 or not glob.glob(os.path.join(d, "**", "c_counter_collection.csv"), recursive=True):
                 raise SystemExit(f"rocprofv3 pass {wl}/{tag} failed ({r.returncode}):\n{r.stdout[-3000:]}")
-    out = parse_counters(out_dir)
+    out = parse_counters(out_dir, only)
     for path in (COUNTERS_FILE, os.path.join(out_dir, "counters.json")):
         with open(path, "w") as f:
             json.dump(out, f, indent=1)
@@ -602,8 +604,9 @@ def _rows(path: str):
                    float(row.get("Counter_Value") or 0.0), int(row.get("Dispatch_Id") or 0))
 
 
-def parse_counters(out_dir: str) -> dict:
-    """profiles/counters.json from the CSVs of collect_counters()."""
+def parse_counters(out_dir: str, only: list[str] | None = None) -> dict:
+    """profiles/counters.json from the CSVs of collect_counters() (with `only`,
+    the other workloads keep their entries of the existing file)."""
     import glob
 
     def csv_of(wl, tag):
@@ -612,9 +615,16 @@ def parse_counters(out_dir: str) -> dict:
     res = {"formula": {"traffic": "FETCH_SIZE and WRITE_SIZE (KiB per dispatch) over the same counter's KiB per "
                                   "byte for torch.neg over 256 MiB of fp32 in the same run",
                        "mfma_busy": "SQ_VALU_MFMA_BUSY_CYCLES / (4 * CUs * GRBM_GUI_ACTIVE / XCDs)",
-                       "mfma_flops_issued": "SQ_INSTS_VALU_MFMA_MOPS_BF16 * 512"},
+                       "mfma_flops_issued": "(SQ_INSTS_VALU_MFMA_MOPS_BF16 + SQ_INSTS_VALU_MFMA_MOPS_F16) * 512"},
            "cus": 256, "xcds": 8, "command": "python bench.py --collect-counters OUT"}
+    if only:
+        old = load_counters()
+        for wl in PMC_WORKLOADS:
+            if wl not in only and wl in old:
+                res[wl] = old[wl]
     for wl, pat in PMC_WORKLOADS.items():
+        if only and wl not in only:
+            continue
         ent = {"kernel": pat or "all kernels of one forward"}
         for tag in ("fetch", "write", "mfma"):
             per = {}  # counter -> (sum over the workload's dispatches, dispatches)
@@ -647,7 +657,8 @@ def parse_counters(out_dir: str) -> dict:
                 ent["mfma_busy_simd_cycles"] = busy
                 ent["grbm_gui_active"] = gui
                 ent["sq_busy_cu_cycles"] = per["SQ_BUSY_CU_CYCLES"][0] / launches
-                ent["mfma_flops_issued"] = per["SQ_INSTS_VALU_MFMA_MOPS_BF16"][0] / launches * 512
+                mops = per.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", (0.0, 0))[0] + per.get("SQ_INSTS_VALU_MFMA_MOPS_F16", (0.0, 0))[0]
+                ent["mfma_flops_issued"] = mops / launches * 512
                 ent["mfma_busy"] = round(busy / (4 * res["cus"] * gui / res["xcds"]), 4) if gui else None
         ent["bytes"] = ent["read_bytes"] + ent["write_bytes"]
         res[wl] = ent
@@ -680,6 +691,8 @@ def main() -> int:
                     help=f"run every counter pass under rocprofv3 into OUT and write "
                          f"{os.path.relpath(COUNTERS_FILE, ROOT)}")
     ap.add_argument("--parse-counters", metavar="OUT", help="rewrite the counters file from an earlier OUT")
+    ap.add_argument("--workloads", default=None,
+                    help="with --collect-counters: only these comma-separated workloads (the others keep their entries)")
     args = ap.parse_args()
     if args.parse_counters:
         out = parse_counters(os.path.abspath(args.parse_counters))
@@ -688,7 +701,10 @@ def main() -> int:
         print(json.dumps(out))
         return 0
     if args.collect_counters:  # spawns the profiled runs; this process never touches the GPU
-        print(json.dumps(collect_counters(args.collect_counters)))
+        only = args.workloads.split(",") if args.workloads else None
+        if only and any(w not in PMC_WORKLOADS for w in only):
+            raise SystemExit(f"unknown workload in {only}; known: {sorted(PMC_WORKLOADS)}")
+        print(json.dumps(collect_counters(args.collect_counters, only)))
         return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py measures one GPU: the kernel set has no multi-GPU path (asked for {args.gpus} GPUs).",
