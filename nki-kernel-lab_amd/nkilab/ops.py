@@ -417,8 +417,10 @@ def attention_into(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.T
     return o
 
 
-def attention(q, k, v, variant: str = "flash_pipelined"):
-    """Causal attention. q, k, v: [H, S, d] (ops.py:77-91); scale 1/sqrt(d).
+def attention(q, k, v, variant: str = "flash_pipelined", scale: float | None = None):
+    """Causal attention. q, k, v: [H, S, d] (ops.py:77-91); scale 1/sqrt(d)
+    unless given (the kernel-level entry points of nkilab.kernels.attention
+    pass theirs).
     k and v may also have fewer heads Hkv dividing H (grouped-query attention:
     query head h uses K/V head h // (H / Hkv)), which the reference lacks.
 
@@ -444,7 +446,7 @@ def attention(q, k, v, variant: str = "flash_pipelined"):
     if dp != d:
         tq, tk, tv = (torch.nn.functional.pad(t, (0, dp - d)) for t in (tq, tk, tv))
     o = torch.empty((H, S, dp), dtype=tq.dtype, device=tq.device)
-    attention_into(tq, tk, tv, o, variant=spec.name, scale=1.0 / math.sqrt(d))
+    attention_into(tq, tk, tv, o, variant=spec.name, scale=1.0 / math.sqrt(d) if scale is None else float(scale))
     if dp != d:
         o = o[:, :, :d].contiguous()
     return from_device(o, kind)

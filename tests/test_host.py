@@ -203,6 +203,48 @@ def test_api_surface_matches_reference_names():
     assert (cfg.d_model, cfg.n_heads, cfg.d_ff, cfg.eps, cfg.head_dim) == (256, 4, 1024, 1e-6, 64)
 
 
+def test_kernels_module_surface():
+    """The kernel-level modules the reference's callers import
+    (tests/test_matmul.py:10, bench/run_bench.py:34-36): tile constants,
+    kernel names, and the blocked matmul's PSUM check raising before any
+    launch (tests/test_matmul.py:34-38)."""
+    from nkilab.kernels import attention as attn
+    from nkilab.kernels import matmul as mm
+    from nkilab.kernels import norm, simulate
+
+    assert (mm.TK, mm.TM, mm.TN, attn.T, norm.P) == (128, 128, 512, 128, 128)
+    for name in ("matmul_naive", "matmul_blocked"):
+        assert callable(getattr(mm, name))
+    for name in ("softmax_unfused", "softmax_fused", "rmsnorm_fused", "swiglu_fused"):
+        assert callable(getattr(norm, name))
+    for name in ("attention_naive", "flash_attention", "flash_attention_kv_resident", "flash_attention_balanced",
+                 "flash_attention_pipelined"):
+        assert callable(getattr(attn, name))
+    lhsT = np.zeros((128, 384), np.float32)
+    rhs = np.zeros((128, 1536), np.float32)
+    with pytest.raises(Exception, match="PSUM"):
+        simulate(mm.matmul_blocked)(lhsT, rhs, BM=3, BN=3)
+
+
+def test_fp16_dtype_code_and_policy_names():
+    import torch
+
+    from nkilab import _lib, model
+    from nkilab._tensors import dtype_code
+
+    assert (_lib.F32, _lib.BF16, _lib.F16) == (0, 1, 2)
+    assert dtype_code(torch.float16) == 2
+    hdr = open(os.path.join(ROOT, "include", "nkilab_hip.h")).read()
+    assert "NKL_F16 = 2" in hdr
+    assert model._DTYPES["float16"] == torch.float16
+    L = _lib.lib()
+    # fp16 operands: the naive GEMM variant and the naive attention refuse them (no launch)
+    assert L.nkl_gemm(None, None, None, None, 4, 4, 4, 4, 4, 4, 0, 0, 1, 0, 0, 0, 0, 2, 2, 1, None) in (-1, -2)
+    assert L.nkl_attention_naive(None, None, None, None, None, 1 << 20, 1, 16, 64, 64, 64, 64, 64, 64, 64, 64, 64,
+                                 ctypes.c_float(0.1), 2, None) == -2
+    assert L.nkl_flash_attn_causal_workspace_bytes(8, 2048, 128, 2) > 0
+
+
 def test_host_validation_happens_before_the_gpu():
     from nkilab import ops
 
