@@ -74,6 +74,12 @@ struct Layout {
   static constexpr int XBYTES = NT * WPT * SLOT * 4;       // team hand-over area (reuses the stages)
   // bf16 elements of LDS (a single team hands nothing over)
   static constexpr int SMEM = NT == 1 || TOTAL * 2 > XBYTES ? TOTAL : XBYTES / 2;
+  // The first segment's Q block, staged in LDS with the K row stride: past
+  // the stages where it fits, else in team 0's second stage (read into
+  // registers before the first tile's barrier, ahead of any write there);
+  // -1: loaded straight into registers.
+  static constexpr int QELEMS = QB * LDK;
+  static constexpr int QOFF = NT == 1 ? -1 : TOTAL + QELEMS <= SMEM ? TOTAL : QELEMS <= STAGE ? STAGE : -1;
 };
 
 
@@ -185,9 +191,40 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
   Seg cur = decode(u1 - 1);
   bf16x8 qf[NQF];
   uint4 rk[CH], rv[CH];  // the next tile's K and V on their way to LDS
-  load_q(cur, qf);
-  gload(cur, 0, p.k, p.k_sh, p.k_ss, goff_k, rk);
-  gload(cur, 0, p.v, p.v_sh, p.v_ss, goff_v, rv);
+  if constexpr (L::QOFF >= 0) {
+    // The first segment's Q block is loaded once for the workgroup, 16
+    // contiguous bytes per lane (four 256-byte rows per wavefront
+    // instruction), and staged in LDS: loaded into registers in the MFMA
+    // operand layout, every wavefront instruction would touch 32 rows and
+    // every team would load the block again.  (Later segments load their Q
+    // while the previous segment ends, off the critical path.)
+    constexpr int QCHUNKS = QB * CPR, QCH = (QCHUNKS + TT * NT - 1) / (TT * NT);  // chunks per thread
+    const int qrows = max(0, min(QB, S - QB * cur.b));
+    const __amdgpu_buffer_rsrc_t qsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(static_cast<const bf16*>(p.q) + (long)cur.hh * p.q_sh + (long)QB * cur.b * p.q_ss), (short)0,
+        qrows > 0 ? 2 * ((qrows - 1) * (int)p.q_ss + dlim) : 0, kBufferFlags);
+    uint4 qc[QCH];
+#pragma unroll
+    for (int i = 0; i < QCH; ++i) {
+      const int ci = min(tid + TT * NT * i, QCHUNKS - 1), row = ci / CPR, col = (ci % CPR) * 8;
+      qc[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(qsrc, 2 * (row * (int)p.q_ss + col), 0, 0));
+    }
+    gload(cur, 0, p.k, p.k_sh, p.k_ss, goff_k, rk);
+    gload(cur, 0, p.v, p.v_sh, p.v_ss, goff_v, rv);
+#pragma unroll
+    for (int i = 0; i < QCH; ++i) {
+      const int ci = tid + TT * NT * i, row = ci / CPR, col = (ci % CPR) * 8;
+      if (QCHUNKS % (TT * NT) == 0 || ci < QCHUNKS)
+        *reinterpret_cast<uint4*>(smem + L::QOFF + row * L::LDK + col) = col < dlim ? qc[i] : make_uint4(0, 0, 0, 0);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int f = 0; f < NQF; ++f) qf[f] = load_frag(smem + L::QOFF + (32 * wq + l32) * L::LDK + 16 * f + 8 * h32);
+  } else {
+    load_q(cur, qf);
+    gload(cur, 0, p.k, p.k_sh, p.k_ss, goff_k, rk);
+    gload(cur, 0, p.v, p.v_sh, p.v_ss, goff_v, rv);
+  }
 
   for (;;) {
     const int hh = cur.hh, b = cur.b, t0 = cur.t0, t1 = cur.t1, nt_b = cur.nt;
