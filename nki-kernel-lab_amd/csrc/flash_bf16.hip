@@ -1206,7 +1206,7 @@ Work plan(int H, int S, Config cfg) {
     const bool pipelined = cfg.kern == kW32x4 || cfg.kern == kW64x2 || cfg.kern == kW64x4 || cfg.kern == kW32x4x2;
     const long nblocks = (long)H * w.nqb;
     const bool few = nblocks < w.grid;
-    int cpb = fwd ? 4 : pipelined ? 2 : cfg.qb == 64 ? (few ? 14 : 10) : (few ? 12 : 4);
+    int cpb = fwd ? (few ? 4 : 2) : pipelined ? 2 : cfg.qb == 64 ? (few ? 14 : 10) : (few ? 12 : 4);
     if (overrides().cpb >= 0) cpb = overrides().cpb;
     while (cpb > 0 && (w.units + nblocks * cpb) / w.grid < cpb + 1) --cpb;
     w.cpb = cpb < 0 ? 0 : cpb;
@@ -1237,8 +1237,12 @@ Work plan(int H, int S, Config cfg) {
 
 // Schedule and kernel choice, from measured launches on MI355X (units of
 // 128-query blocks per CU): below 12, 64-query blocks halve the unit and keep
-// every CU busy (1 x 4096: 8); up to 200 the 8-wavefront teams kernel over
-// balanced ranges (whole blocks leave CUs idle or unevenly loaded); from 200
+// every CU busy (1 x 4096: 8); up to 48 the 8-wavefront teams kernel over
+// balanced ranges (whole blocks leave CUs idle or unevenly loaded; 6 x 2048:
+// 24.5 us against 27.2 for the ping-pong kernel, 12 x 2048 30.8 against
+// 31.6); up to 200 the ping-pong 64-key-tile kernel (flash_fwd.hip) for
+// d > 64, whose steady state is faster (8 x 4096 48.5 against 49.4 us,
+// 4 x 8192 81.0 against 83.9; the teams kernel takes d <= 64 and fp16); from 200
 // the software-pipelined kernel at two wavefronts per SIMD (d > 64), whose
 // steady state is faster and whose longer segments amortise its start-up;
 // from 1024 one workgroup per pair of blocks, which balances as well and
@@ -1250,7 +1254,8 @@ Config choose(int H, int S, int d, bool f16) {
   const long nqb = (S + 127) / 128;
   const long units128 = (long)H * (2 * (nqb - 1) * nqb + (S - 1) / BN + 1);
   Config cfg = units128 < 12 * cus     ? Config{64, kBalanced, kTeams}
-               : units128 < 200 * cus  ? Config{128, kBalanced, kTeams}
+               : units128 < 48 * cus   ? Config{128, kBalanced, kTeams}
+               : units128 < 200 * cus  ? Config{128, kBalanced, kFwdPP}
                : units128 < 1024 * cus ? Config{128, kBalanced, kW32x4x2}
                                        : Config{128, kPairs, kW32x4x2};
   const Overrides& ov = overrides();

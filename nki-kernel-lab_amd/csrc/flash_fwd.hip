@@ -187,9 +187,42 @@ void flash_fwd_kernel(AttnArgs p, Work w) {
 
   Seg cur = decode_seg(u1 - 1, u0, w);
   Src src = seg_src(cur);
-  load_q(cur);
-  dma(src, 0);
-  if (cur.t1 - cur.t0 > 1) dma(src, 1);
+  if constexpr (PP) {
+    // The first segment's Q block is copied once for the workgroup into the
+    // K halves of stages 2 and 3 (16 rows per wavefront, swizzled like the K
+    // rows), which no copy writes before the first tile's barrier; the two
+    // wavefronts of each SIMD read their Q fragments from there.  (Loaded
+    // into registers in the MFMA operand layout, each wavefront instruction
+    // would touch 32 rows, and both wavefronts of a SIMD would load them.
+    // Later segments load their Q while the previous segment ends.)
+    const int qrows = max(0, min(QB, S - QB * cur.b));
+    const __amdgpu_buffer_rsrc_t qsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(static_cast<const bf16*>(p.q) + (long)cur.hh * p.q_sh + (long)QB * cur.b * p.q_ss), (short)0,
+        qrows > 0 ? 2 * ((qrows - 1) * (int)p.q_ss + dlim) : 0, kBufferFlags);
+    const unsigned qbase = (unsigned)(size_t)(const __attribute__((address_space(3))) void*)lds + 2 * TILEB + 4096 * wid;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int row = 4 * (4 * wid + u) + (lane >> 4);
+      const int lc = (lane & 15) ^ row_swz(row);
+      copy_1k(qsrc, lc * 8 < dlim ? 2 * (row * (int)p.q_ss + lc * 8) : 0x40000000, qbase + 1024 * u);
+    }
+    dma(src, 0);
+    if (cur.t1 - cur.t0 > 1) {
+      dma(src, 1);
+      wait_vm<8>();  // this wavefront's Q copies have landed
+    } else {
+      wait_vm<4>();
+    }
+    bar();  // and every wavefront's; the first tile's barrier follows these reads
+#pragma unroll
+    for (int f = 0; f < 8; ++f)
+      qf[f] = *reinterpret_cast<const bf16x8*>(lds + 2 * TILEB + (32 * wq + l32) * ROWB +
+                                               (((2 * f + h32) ^ row_swz(l32)) << 4));
+  } else {
+    load_q(cur);
+    dma(src, 0);
+    if (cur.t1 - cur.t0 > 1) dma(src, 1);
+  }
 
   for (;;) {
     const int hh = cur.hh, b = cur.b, t0 = cur.t0, nt = cur.t1 - cur.t0;
