@@ -497,7 +497,8 @@ COUNTER_SETS = {"fetch": ["FETCH_SIZE"], "write": ["WRITE_SIZE"],
 # of the workload but the calibration copy)
 PMC_WORKLOADS = {"attention": "flash", "attention_1x4096": "flash", "attention_32x16384": "flash",
                  "matmul": "gemm", "softmax": "softmax_vec", "rmsnorm": "rmsnorm_vec", "swiglu": "swiglu_vec",
-                 "decoder": "", "gemm_qkv": "gemm", "gemm_wo": "gemm", "gemm_gate_up": "gemm", "gemm_down": "gemm"}
+                 "decoder": "", "gemm_qkv": "gemm", "gemm_wo": "gemm", "gemm_gate_up": "gemm", "gemm_down": "gemm",
+                 "gemm_4096": "gemm", "hipblaslt_4096": "Cijk"}
 # The decoder block's four projections at hidden 2048, FFN 5632, 2048 tokens:
 # (M, N, K); gate/up is the fused GEMM with the SwiGLU epilogue (N = 2 x 5632).
 DECODER_GEMMS = {"gemm_qkv": (2048, 6144, 2048), "gemm_wo": (2048, 2048, 2048), "gemm_gate_up": (2048, 11264, 2048),
@@ -539,8 +540,8 @@ def pmc_pass(workload: str) -> None:
                 ops.rmsnorm_into(x.clone(), w, torch.empty_like(x), 1e-6)
             else:
                 ops.swiglu_into(gate.clone(), up.clone(), torch.empty_like(gate))
-    elif workload in DECODER_GEMMS:
-        M, N, K = DECODER_GEMMS[workload]
+    elif workload in DECODER_GEMMS or workload in ("gemm_4096", "hipblaslt_4096"):
+        M, N, K = DECODER_GEMMS.get(workload, (4096, 4096, 4096))
         g = torch.Generator().manual_seed(0)
         a = (torch.randn(M, K, generator=g) * 1.0).to(torch.bfloat16).cuda()
         sets = []
@@ -554,6 +555,8 @@ def pmc_pass(workload: str) -> None:
         for i in range(PMC_REPS):
             if workload == "gemm_gate_up":
                 ops.gemm_swiglu_into(*sets[i % 4])
+            elif workload == "hipblaslt_4096":  # torch.mm: the hipBLASLt kernel on the same operands
+                torch.mm(sets[i % 4][0], sets[i % 4][1].t(), out=sets[i % 4][2])
             else:
                 ops.linear_into(*sets[i % 4])
     elif workload == "decoder":
