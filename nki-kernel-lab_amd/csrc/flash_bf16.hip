@@ -188,42 +188,64 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
     }
   };
 
-  Seg cur = decode(u1 - 1);
-  bf16x8 qf[NQF];
-  uint4 rk[CH], rv[CH];  // the next tile's K and V on their way to LDS
-  if constexpr (L::QOFF >= 0) {
-    // The first segment's Q block is loaded once for the workgroup, 16
-    // contiguous bytes per lane (four 256-byte rows per wavefront
-    // instruction), and staged in LDS: loaded into registers in the MFMA
-    // operand layout, every wavefront instruction would touch 32 rows and
-    // every team would load the block again.  (Later segments load their Q
-    // while the previous segment ends, off the critical path.)
-    constexpr int QCHUNKS = QB * CPR, QCH = (QCHUNKS + TT * NT - 1) / (TT * NT);  // chunks per thread
-    const int qrows = max(0, min(QB, S - QB * cur.b));
+  // Every wavefront's LDS accesses are done, then all wavefronts meet.  A
+  // bare barrier: __syncthreads()' fence would also wait for every
+  // outstanding global load (vmcnt(0)) -- the next tile's K/V in the loop,
+  // the next segment's Q and first tile at a segment end -- which the
+  // registers they land in are waited for where they are used.
+  auto lds_barrier = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  };
+
+  // A segment's Q block is loaded once for the workgroup, 16 contiguous
+  // bytes per lane (four 256-byte rows per wavefront instruction), and staged
+  // in LDS, where each wavefront reads its MFMA fragments: loaded into
+  // registers in the operand layout, every wavefront instruction would touch
+  // 32 rows and every team would load the block again.  Past the stages
+  // (QLA) the staging area is free at every segment start; in team 0's
+  // second stage only the first segment's Q goes through it (later ones are
+  // loaded straight into registers).
+  constexpr bool QL = L::QOFF >= 0, QLA = L::QOFF == L::TOTAL;
+  constexpr int QCHUNKS = QB * CPR, QCH = (QCHUNKS + TT * NT - 1) / (TT * NT);  // chunks per thread
+  uint4 qc[QCH];
+  auto load_qc = [&](const Seg& sg) __attribute__((always_inline)) {
+    const int qrows = max(0, min(QB, S - QB * sg.b));
     const __amdgpu_buffer_rsrc_t qsrc = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(static_cast<const bf16*>(p.q) + (long)cur.hh * p.q_sh + (long)QB * cur.b * p.q_ss), (short)0,
+        (void*)(static_cast<const bf16*>(p.q) + (long)sg.hh * p.q_sh + (long)QB * sg.b * p.q_ss), (short)0,
         qrows > 0 ? 2 * ((qrows - 1) * (int)p.q_ss + dlim) : 0, kBufferFlags);
-    uint4 qc[QCH];
 #pragma unroll
     for (int i = 0; i < QCH; ++i) {
       const int ci = min(tid + TT * NT * i, QCHUNKS - 1), row = ci / CPR, col = (ci % CPR) * 8;
       qc[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(qsrc, 2 * (row * (int)p.q_ss + col), 0, 0));
     }
-    gload(cur, 0, p.k, p.k_sh, p.k_ss, goff_k, rk);
-    gload(cur, 0, p.v, p.v_sh, p.v_ss, goff_v, rv);
+  };
+  auto store_qc = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < QCH; ++i) {
       const int ci = tid + TT * NT * i, row = ci / CPR, col = (ci % CPR) * 8;
       if (QCHUNKS % (TT * NT) == 0 || ci < QCHUNKS)
         *reinterpret_cast<uint4*>(smem + L::QOFF + row * L::LDK + col) = col < dlim ? qc[i] : make_uint4(0, 0, 0, 0);
     }
-    __syncthreads();
+  };
+  auto read_qf = [&](bf16x8 (&q)[NQF]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int f = 0; f < NQF; ++f) qf[f] = load_frag(smem + L::QOFF + (32 * wq + l32) * L::LDK + 16 * f + 8 * h32);
-  } else {
-    load_q(cur, qf);
-    gload(cur, 0, p.k, p.k_sh, p.k_ss, goff_k, rk);
-    gload(cur, 0, p.v, p.v_sh, p.v_ss, goff_v, rv);
+    for (int f = 0; f < NQF; ++f) q[f] = load_frag(smem + L::QOFF + (32 * wq + l32) * L::LDK + 16 * f + 8 * h32);
+  };
+
+  Seg cur = decode(u1 - 1);
+  bf16x8 qf[NQF];
+  uint4 rk[CH], rv[CH];  // the next tile's K and V on their way to LDS
+  if constexpr (QL) load_qc(cur);
+  else load_q(cur, qf);
+  gload(cur, 0, p.k, p.k_sh, p.k_ss, goff_k, rk);
+  gload(cur, 0, p.v, p.v_sh, p.v_ss, goff_v, rv);
+  if constexpr (QL && !QLA) {  // staged in team 0's second stage: read before the first tile's barrier
+    store_qc();
+    __syncthreads();
+    read_qf(qf);
   }
 
   for (;;) {
@@ -233,8 +255,10 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
     const int myq = qw + l32;
     const int nit = (t1 - t0 + NT - 1) / NT;
 
+    if constexpr (QLA) store_qc();
     lstore(0, rk, rv);
-    __syncthreads();
+    lds_barrier();
+    if constexpr (QLA) read_qf(qf);
     gload(cur, 1, p.k, p.k_sh, p.k_ss, goff_k, rk);
     gload(cur, 1, p.v, p.v_sh, p.v_ss, goff_v, rv);
 
@@ -339,7 +363,7 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
           __builtin_amdgcn_sched_barrier(0);
           pv(sb, pf);
         }
-        __syncthreads();
+        lds_barrier();
       }
     }
 
@@ -353,7 +377,10 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
     Seg nxt = cur;
     if (more) nxt = decode(next_u);
     if (more) {
-      load_q(nxt, qf);  // this segment's Q fragments are no longer needed
+      if constexpr (QLA)
+        load_qc(nxt);
+      else
+        load_q(nxt, qf);  // this segment's Q fragments are no longer needed
       gload(nxt, 0, p.k, p.k_sh, p.k_ss, goff_k, rk);
       gload(nxt, 0, p.v, p.v_sh, p.v_ss, goff_v, rv);
     }
@@ -385,7 +412,7 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
       if (team == t && t * OWN < NDB)
 #pragma unroll
         for (int j = 0; j < OWN; ++j) own[j] = oacc[t * OWN + j < NDB ? t * OWN + j : NDB - 1];
-    if constexpr (NT > 1) __syncthreads();
+    if constexpr (NT > 1) lds_barrier();
 
     // Folds a state with max m2 and sum l2 into (m_run, l_tot) and returns the
     // weights of the running state (a1) and of the other (a2).  An empty state
@@ -561,7 +588,7 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
         if (tid == 0) atomicExch(&w.count[hh * w.nqb + b], 0);
       }
     }
-    __syncthreads();  // the LDS is restaged by the next segment
+    lds_barrier();  // the LDS is restaged by the next segment
     if (!more) break;
     cur = nxt;
   }
@@ -1197,16 +1224,17 @@ Work plan(int H, int S, Config cfg) {
     // Block start cost, in units: about a segment's fixed work over the time
     // of one unit in the loop, tuned on MI355X with rotating inputs.  With
     // fewer blocks than workgroups every block is split and a higher cost
-    // pays (teams kernel, 128-query blocks: 8 x 2048 28.9 -> 27.0 us at 12
-    // against 4; 12 x 2048 40.1 -> 34.4; 2 x 8192 57.3 -> 53.7); with at least
-    // as many, 4 is best (16 x 2048, 8 x 4096, 4 x 8192).  64-query blocks:
+    // pays (teams kernel, 128-query blocks: 6 against 12 since every
+    // segment's Q is staged in LDS, 8 x 2048 25.3 -> 24.4-24.8 us, 12 x 2048
+    // 31.5 -> 29.9, 6 x 2048 24.6 -> 24.0); with at least as many, 4 is best
+    // (16 x 2048, 8 x 4096, 4 x 8192).  64-query blocks:
     // 14 and 10 (1 x 4096: 32.3 -> 24.6 us against no cost); the pipelined
     // kernel's longer segments gain little.  At most a range's cost minus
     // one, so that every range holds a unit.
     const bool pipelined = cfg.kern == kW32x4 || cfg.kern == kW64x2 || cfg.kern == kW64x4 || cfg.kern == kW32x4x2;
     const long nblocks = (long)H * w.nqb;
     const bool few = nblocks < w.grid;
-    int cpb = fwd ? (few ? 4 : 2) : pipelined ? 2 : cfg.qb == 64 ? (few ? 14 : 10) : (few ? 12 : 4);
+    int cpb = fwd ? (few ? 4 : 2) : pipelined ? 2 : cfg.qb == 64 ? (few ? 14 : 10) : (few ? 6 : 4);
     if (overrides().cpb >= 0) cpb = overrides().cpb;
     while (cpb > 0 && (w.units + nblocks * cpb) / w.grid < cpb + 1) --cpb;
     w.cpb = cpb < 0 ? 0 : cpb;
