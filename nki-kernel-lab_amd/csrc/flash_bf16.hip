@@ -1228,13 +1228,14 @@ Work plan(int H, int S, Config cfg) {
     // segment's Q is staged in LDS, 8 x 2048 25.3 -> 24.4-24.8 us, 12 x 2048
     // 31.5 -> 29.9, 6 x 2048 24.6 -> 24.0); with at least as many, 4 is best
     // (16 x 2048, 8 x 4096, 4 x 8192).  64-query blocks:
-    // 14 and 10 (1 x 4096: 32.3 -> 24.6 us against no cost); the pipelined
+    // 18 and 10 (1 x 4096: 32.3 -> 24.6 us at 14 against no cost, 23.4 ->
+    // 23.0 at 18; 4 x 2048 21.4 -> 20.5); the pipelined
     // kernel's longer segments gain little.  At most a range's cost minus
     // one, so that every range holds a unit.
     const bool pipelined = cfg.kern == kW32x4 || cfg.kern == kW64x2 || cfg.kern == kW64x4 || cfg.kern == kW32x4x2;
     const long nblocks = (long)H * w.nqb;
     const bool few = nblocks < w.grid;
-    int cpb = fwd ? (few ? 4 : 2) : pipelined ? 2 : cfg.qb == 64 ? (few ? 14 : 10) : (few ? 6 : 4);
+    int cpb = fwd ? (few ? 4 : 2) : pipelined ? 2 : cfg.qb == 64 ? (few ? 18 : 10) : (few ? 6 : 4);
     if (overrides().cpb >= 0) cpb = overrides().cpb;
     while (cpb > 0 && (w.units + nblocks * cpb) / w.grid < cpb + 1) --cpb;
     w.cpb = cpb < 0 ? 0 : cpb;
