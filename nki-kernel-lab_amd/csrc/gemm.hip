@@ -296,10 +296,14 @@ constexpr unsigned kOOB = 0x80000000u;  // a buffer offset past every range: the
 
 }  // namespace
 
-template <typename TI, typename TO, int BM, int BN, bool BT, int NS, int WGM = 2, int WGN = 2>
-__global__ __launch_bounds__(64 * WGM * WGN) void gemm_dma_kernel(GemmArgs p) {
+template <typename TI, typename TO, int BM, int BN, bool BT, int NS, int WGM = 2, int WGN = 2, int KG = 1>
+__global__ __launch_bounds__(64 * WGM * WGN * KG) void gemm_dma_kernel(GemmArgs p) {
   // TI: the 16-bit operand format (bf16 or fp16); operands move as raw 16-bit
   // values, the format only picks the MFMA.
+  // KG > 1: KG groups of WGM x WGN wavefronts share the tile; group g takes
+  // K-steps g, g + KG, ... through its own part of each stage, and the groups'
+  // accumulators are added in group order at the end.  Each SIMD then runs KG
+  // wavefronts whose copy and fragment-read latencies hide each other's.
   constexpr bool H = std::is_same<TI, f16>::value;
   static_assert(H || std::is_same<TI, bf16>::value, "16-bit operands");
   constexpr int NW = WGM * WGN;
@@ -313,10 +317,13 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_dma_kernel(GemmArgs p) {
                 "tile too small");
   static_assert(TM >= 1 && TN >= 1 && TM * 32 * WGM == BM && TN * 32 * WGN == BN, "wavefront tiles");
   static_assert((NS - 2) * LPT < 64, "vmcnt range");
-  __shared__ __align__(16) unsigned char lds[NS * STAGE];
+  static_assert(KG >= 1, "K groups");
+  constexpr int SSET = KG * STAGE;  // one stage of every group
+  __shared__ __align__(16) unsigned char lds[NS * SSET];
 
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wall = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kg = wall / NW, wid = wall % NW;  // K group, wavefront within it
   const int wm = wid / WGN, wn = wid % WGN;
   const int tiles_m = (p.M + BM - 1) / BM, tiles_n = (p.N + BN - 1) / BN;
   int tm, tn;
@@ -378,8 +385,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_dma_kernel(GemmArgs p) {
   // Copy instruction u (A for u < A_PW, then B) of K-step s into stage st
   // (K-steps past K copy zeros).
   auto dma1 = [&](int s, int st, int u) __attribute__((always_inline)) {
-    const int k0 = s * G_BK;
-    unsigned char* sb = lds + st * STAGE;
+    const int k0 = (KG * s + kg) * G_BK;
+    unsigned char* sb = lds + st * SSET + kg * STAGE;
     if (u < A_PW) {
       const unsigned off = (aoff[u] != kOOB && k0 + akc[u] < K) ? aoff[u] + 2u * k0 : kOOB;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (__attribute__((address_space(3))) void*)(sb + (wid * A_PW + u) * 1024),
@@ -505,16 +512,18 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_dma_kernel(GemmArgs p) {
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  const int nk = (K + G_BK - 1) / G_BK;
+  // Steps of the loop: KG K-steps each (a group's K-steps past K copy zeros).
+  const int nk = ((K + G_BK - 1) / G_BK + KG - 1) / KG;
+  const unsigned char* const glds = lds + kg * STAGE;  // this group's part of stage 0
 #pragma unroll
   for (int s = 0; s < (SPREAD ? NS - 1 : NS); ++s) dma(s, s);
   g_wait_vm<(SPREAD ? NS - 2 : NS - 1) * LPT>();  // K-step 0 has landed
   barrier();
   bf16x8 fa[2][TM], fb[2][TN];
-  frags(lds, 0, fa[0], fb[0]);
+  frags(glds, 0, fa[0], fb[0]);
 #pragma unroll 1
   for (int s = 0; s < nk; ++s) {
-    const unsigned char* sb = lds + (s % NS) * STAGE;
+    const unsigned char* sb = glds + (s % NS) * SSET;
 #pragma unroll
     for (int ks = 0; ks < 3; ++ks) {
       if constexpr (!BT) {  // B^T fragments of sub-step ks have landed (read one sub-step ago)
@@ -539,13 +548,53 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_dma_kernel(GemmArgs p) {
     // The next K-step's first fragment reads come first in program order
     // (the copies may alias them), then the last sub-step's MFMAs, whose
     // fragments are already in registers.
-    frags(lds + ((s + 1) % NS) * STAGE, 0, fa[0], fb[0]);
+    frags(glds + ((s + 1) % NS) * SSET, 0, fa[0], fb[0]);
     if constexpr (SPREAD)
       mma_copy(fa[1], fb[1], s + NS - 1, 3 * Q, LPT);
     else
       mma_copy(fa[1], fb[1], s + NS, 0, LPT);  // into K-step s's stage
   }
   __builtin_amdgcn_s_waitcnt(0);  // the copies of K-steps past K have landed
+
+  // Epilogue staging (staged path): NW wavefronts x RP rows of PITCH floats.
+  constexpr int OE = 16 / sizeof(TO);  // output elements per 16-byte store
+  constexpr int WC_MAX = WN;           // staged columns per wavefront (SwiGLU: WN / 2)
+  constexpr int PITCH = WC_MAX + 4;    // staged row pitch, floats
+  constexpr int RP = NW * WM * PITCH * 4 <= NS * SSET ? WM : 32;  // rows per pass
+  constexpr int TP = RP / 32;                                      // tiles per pass
+  static_assert(NW * RP * PITCH * 4 <= NS * SSET, "the staged rows fit the stages");
+  if constexpr (KG > 1) {
+    // Groups 1 .. KG-1 leave their accumulators in LDS past the staging
+    // area (lane-major float4 chunks); group 0 adds them in group order and
+    // writes the tile alone.  The second barrier is the last one any
+    // wavefront takes part in.
+    constexpr int NCH = TM * TN * 4;  // float4 chunks per lane
+    constexpr int ROFF = (NW * RP * PITCH * 4 + 15) / 16 * 16;
+    static_assert(ROFF + (KG - 1) * NW * NCH * 1024 <= NS * SSET, "the partial sums fit the stages");
+    float4* red = reinterpret_cast<float4*>(lds + ROFF);
+    __syncthreads();  // every wavefront is done with the stages
+    if (kg > 0) {
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        const floatx16& a = acc[c / 4 / TN][c / 4 % TN];
+        red[(((kg - 1) * NW + wid) * NCH + c) * 64 + lane] =
+            make_float4(a[4 * (c % 4)], a[4 * (c % 4) + 1], a[4 * (c % 4) + 2], a[4 * (c % 4) + 3]);
+      }
+    }
+    __syncthreads();
+    if (kg > 0) return;
+#pragma unroll
+    for (int g = 1; g < KG; ++g)
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        const float4 v = red[(((g - 1) * NW + wid) * NCH + c) * 64 + lane];
+        floatx16& a = acc[c / 4 / TN][c / 4 % TN];
+        a[4 * (c % 4)] += v.x;
+        a[4 * (c % 4) + 1] += v.y;
+        a[4 * (c % 4) + 2] += v.z;
+        a[4 * (c % 4) + 3] += v.w;
+      }
+  }
 
   // Epilogue: accumulator element e of tile (i, j) is C[row][col] with
   // row = 8 * (e / 4) + 4 * (lane / 32) + e % 4, col = lane % 32.
@@ -558,13 +607,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_dma_kernel(GemmArgs p) {
     // interleaved in groups of 32), and the block written is
     // silu(TO(gate)) * TO(up): the values a gate and an up GEMM with TO
     // outputs would hand the SwiGLU kernel.
-    constexpr int OE = 16 / sizeof(TO);  // output elements per 16-byte store
-    constexpr int WC_MAX = WN;           // staged columns per wavefront (SwiGLU: WN / 2)
-    constexpr int PITCH = WC_MAX + 4;    // staged row pitch, floats
-    constexpr int RP = NW * WM * PITCH * 4 <= NS * STAGE ? WM : 32;  // rows per pass
-    constexpr int TP = RP / 32;                                       // tiles per pass
-    static_assert(NW * RP * PITCH * 4 <= NS * STAGE, "the staged rows fit the stages");
-    __syncthreads();  // every wavefront is done with the stages
+    if constexpr (KG == 1) __syncthreads();  // every wavefront is done with the stages (KG > 1: above)
     float* stg = reinterpret_cast<float*>(lds) + wid * (RP * PITCH);
     const bool sw = p.epi == kEpiSwiglu;
     const int wc = sw ? WN / 2 : WN;
@@ -653,7 +696,9 @@ static bool staged_ok(const GemmArgs& a) {
 }
 
 // Tiles of the LDS-DMA kernel.
-enum DmaTile { kT64x64, kT64x128, kT128x128, kT128x256, kT256x128, kT256x192, kT256x256, kTileCount };
+// K2: two K groups of four wavefronts per tile.
+enum DmaTile { kT64x64, kT64x128, kT128x128, kT128x256, kT256x128, kT256x192, kT256x256, kT64x64K2, kT64x128K2,
+               kTileCount };
 
 template <typename TI, typename TO, bool BT>
 static void launch_dma(DmaTile t, const GemmArgs& g, int batch, hipStream_t st) {
@@ -667,17 +712,20 @@ static void launch_dma(DmaTile t, const GemmArgs& g, int batch, hipStream_t st) 
     case kT128x256: gemm_dma_kernel<TI, TO, 128, 256, BT, 3, 2, 4><<<grid(128, 256), dim3(512), 0, st>>>(g); break;
     case kT128x128: gemm_dma_kernel<TI, TO, 128, 128, BT, 4><<<grid(128, 128), dim3(256), 0, st>>>(g); break;
     case kT64x128: gemm_dma_kernel<TI, TO, 64, 128, BT, 6><<<grid(64, 128), dim3(256), 0, st>>>(g); break;
+    case kT64x128K2: gemm_dma_kernel<TI, TO, 64, 128, BT, 3, 2, 2, 2><<<grid(64, 128), dim3(512), 0, st>>>(g); break;
+    case kT64x64K2: gemm_dma_kernel<TI, TO, 64, 64, BT, 4, 2, 2, 2><<<grid(64, 64), dim3(512), 0, st>>>(g); break;
     default: gemm_dma_kernel<TI, TO, 64, 64, BT, 8><<<grid(64, 64), dim3(256), 0, st>>>(g); break;
   }
 }
 
-// NKL_GEMM_TILE=64x64|64x128|128x128|128x256|256x128|256x256 forces a tile
-// (for measurements); -1 when unset or unknown.
+// NKL_GEMM_TILE=64x64|64x128|128x128|128x256|256x128|256x192|256x256|64x64k2|64x128k2
+// forces a tile (for measurements); -1 when unset or unknown.
 static int forced_tile() {
   static const int forced = [] {
     const char* f = getenv("NKL_GEMM_TILE");
     if (!f) return -1;
-    static const char* names[kTileCount] = {"64x64", "64x128", "128x128", "128x256", "256x128", "256x192", "256x256"};
+    static const char* names[kTileCount] = {"64x64",   "64x128",   "128x128",  "128x256", "256x128",
+                                            "256x192", "256x256", "64x64k2", "64x128k2"};
     for (int i = 0; i < kTileCount; ++i)
       if (!strcmp(f, names[i])) return i;
     return -1;
@@ -694,7 +742,9 @@ static long tiles_of(const GemmArgs& a, int bm, int bn, int batch) {
 // of a round measured on MI355X (bf16, K-contiguous B): 256x256 1.9 us,
 // 256x192 1.75 us, 256x128 1.25 us, 128x128 0.8 us.  256x192 fills the CUs
 // where 256x256 leaves a quarter idle (2048 x 6144: 256 tiles against 192).
-// Smaller GEMMs: the largest tile that still gives every CU a workgroup.
+// Smaller GEMMs: the largest tile that still gives every CU a workgroup, with
+// two K groups (64x64: 1024^3 9.0 -> 8.4 us; 64x128: 2-6% on 1024-2048-row
+// shapes).
 static DmaTile choose_tile(const GemmArgs& a, int batch) {
   if (forced_tile() >= 0) return (DmaTile)forced_tile();
   const long t128 = tiles_of(a, 128, 128, batch);
@@ -711,8 +761,8 @@ static DmaTile choose_tile(const GemmArgs& a, int batch) {
       if (c.c < cb) cb = c.c, best = c.t;
     return best;
   }
-  if (tiles_of(a, 64, 128, batch) >= 256) return kT64x128;
-  return kT64x64;
+  if (tiles_of(a, 64, 128, batch) >= 256) return kT64x128K2;
+  return kT64x64K2;
 }
 
 template <typename T, typename TO, bool BT>
@@ -817,9 +867,15 @@ extern "C" int nkl_gemm_swiglu(const void* A, const void* Bgu, void* C, int M, i
     return set_error(NKL_EINVAL, "nkl_gemm_swiglu: operands must be under 2 GiB");
   GemmArgs a{A, Bgu, C, nullptr, M, 2 * N, K, lda, ldb, ldc, 0, 0, 0, 0, 0, kEpiSwiglu};
   hipStream_t st = (hipStream_t)stream;
-  // A tile whose wavefronts own 64 columns: one gate/up pair.
-  DmaTile t = choose_tile(a, 1);
+  // A tile whose wavefronts own 64 columns (one gate/up pair), summing the
+  // K-steps in the order the separate M x N gate and up GEMMs would: in two
+  // K groups where their tile has them.
+  GemmArgs half = a;
+  half.N = N;
+  const DmaTile th = choose_tile(half, 1);
+  DmaTile t = th == kT64x64K2 || th == kT64x128K2 ? kT64x128K2 : choose_tile(a, 1);
   if (t == kT64x64) t = kT64x128;
+  if (t == kT64x64K2) t = kT64x128K2;
   if (t == kT256x192) t = kT256x256;
   if (dtype == NKL_F16)
     launch_dma<f16, f16, true>(t, a, 1, st);
