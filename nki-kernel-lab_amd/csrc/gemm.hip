@@ -765,6 +765,95 @@ static DmaTile choose_tile(const GemmArgs& a, int batch) {
   return kT64x64K2;
 }
 
+// CUs of the current device (256 on MI355X), read once per device.
+static int gemm_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// Rows and columns of a tile.
+static void tile_dims(DmaTile t, int& bm, int& bn) {
+  switch (t) {
+    case kT256x256: bm = 256, bn = 256; break;
+    case kT256x192: bm = 256, bn = 192; break;
+    case kT256x128: bm = 256, bn = 128; break;
+    case kT128x256: bm = 128, bn = 256; break;
+    case kT128x128: bm = 128, bn = 128; break;
+    case kT64x128:
+    case kT64x128K2: bm = 64, bn = 128; break;
+    default: bm = 64, bn = 64; break;
+  }
+}
+
+// Time per K-step of a round of one-per-CU workgroups (the tile choice's
+// figures), 0 for the tiles it does not price.
+static double round_step_us(DmaTile t) {
+  return t == kT256x256 ? 1.9 : t == kT256x192 ? 1.75 : t == kT256x128 ? 1.25 : t == kT128x128 ? 0.8 : 0.0;
+}
+
+// Column split of a launch whose 256-row tiles leave a partial last round:
+// the columns of the whole rounds go to a first launch with that tile, the
+// rest to a second launch with the tile chosen for them alone (2048 x 11264
+// at 256 x 256: 256 tiles, then 96 -- instead, 256 tiles over the first 8192
+// columns and 192 tiles of 256 x 128 over the last 3072).  n1 = 0: no split.
+struct ColSplit {
+  int n1;
+  DmaTile t2;
+};
+static ColSplit col_split(const GemmArgs& a, DmaTile t, int batch, bool swiglu) {
+  ColSplit cs{0, t};
+  int bm, bn;
+  tile_dims(t, bm, bn);
+  if (batch != 1 || forced_tile() >= 0 || bm != 256) return cs;
+  const long cus = gemm_cus(), tm = (a.M + 255) / 256, tiles = tm * ((a.N + bn - 1) / bn);
+  if (tiles <= cus || tiles % cus == 0 || tm > cus) return cs;
+  const long full_tn = (tiles / cus) * cus / tm;  // column tiles of the whole rounds
+  const long n1 = full_tn * bn;
+  if (n1 <= 0 || n1 >= a.N) return cs;
+  GemmArgs rest = a;
+  rest.N = (int)(a.N - n1);
+  DmaTile t2 = choose_tile(rest, 1);
+  if (swiglu && t2 == kT256x192) t2 = kT256x256;  // wavefronts own 64 columns
+  if (round_step_us(t2) == 0.0) return cs;
+  auto rounds = [&](long n) { return (double)((n + cus - 1) / cus); };
+  const double nk = (a.K + G_BK - 1) / G_BK;
+  const double whole = round_step_us(t) * rounds(tiles) * nk;
+  int bm2, bn2;
+  tile_dims(t2, bm2, bn2);
+  const double split = round_step_us(t) * rounds(tm * full_tn) * nk +
+                       round_step_us(t2) * rounds(tiles_of(rest, bm2, bn2, 1)) * nk + 2.0;  // + the second launch
+  if (split < whole) cs = ColSplit{(int)n1, t2};
+  return cs;
+}
+
+// launch_dma over a column split when col_split finds one (swiglu: the
+// gate/up GEMM, whose output has half the columns).
+template <typename TI, typename TO, bool BT>
+static void launch_dma_cols(DmaTile t, const GemmArgs& g, int batch, bool swiglu, hipStream_t st) {
+  const ColSplit cs = col_split(g, t, batch, swiglu);
+  if (cs.n1 == 0) {
+    launch_dma<TI, TO, BT>(t, g, batch, st);
+    return;
+  }
+  GemmArgs g1 = g, g2 = g;
+  g1.N = cs.n1;
+  g2.N = g.N - cs.n1;
+  const uint16_t* B = static_cast<const uint16_t*>(g.B);
+  g2.B = BT ? B + (long)cs.n1 * g.ldb : B + cs.n1;
+  const long coff = swiglu ? cs.n1 / 2 : cs.n1;
+  g2.C = static_cast<TO*>(g.C) + coff;
+  if (g.R) g2.R = static_cast<const TO*>(g.R) + coff;
+  launch_dma<TI, TO, BT>(t, g1, 1, st);
+  launch_dma<TI, TO, BT>(cs.t2, g2, 1, st);
+}
+
 template <typename T, typename TO, bool BT>
 static int gemm_dispatch(const GemmArgs& a, int batch, int variant, hipStream_t st) {
   constexpr int E = VecE<T>::value;
@@ -780,7 +869,7 @@ static int gemm_dispatch(const GemmArgs& a, int batch, int variant, hipStream_t 
                        "and leading dimensions multiples of 8, and operands under 2 GiB");
     GemmArgs g = a;
     g.epi = staged_ok<TO>(a) ? kEpiStaged : kEpiElem;
-    launch_dma<f16, TO, BT>(choose_tile(a, batch), g, batch, st);
+    launch_dma_cols<f16, TO, BT>(choose_tile(a, batch), g, batch, false, st);
     return check_launch("nkl_gemm(blocked)");
   } else {
   if (variant == NKL_GEMM_NAIVE || !vec) {
@@ -797,7 +886,7 @@ static int gemm_dispatch(const GemmArgs& a, int batch, int variant, hipStream_t 
     if (a_bytes < (1L << 31) && b_bytes < (1L << 31)) {
       GemmArgs g = a;
       g.epi = staged_ok<TO>(a) ? kEpiStaged : kEpiElem;
-      launch_dma<bf16, TO, BT>(choose_tile(a, batch), g, batch, st);
+      launch_dma_cols<bf16, TO, BT>(choose_tile(a, batch), g, batch, false, st);
       return check_launch("nkl_gemm(blocked)");
     }
   }
@@ -878,9 +967,9 @@ extern "C" int nkl_gemm_swiglu(const void* A, const void* Bgu, void* C, int M, i
   if (t == kT64x64K2) t = kT64x128K2;
   if (t == kT256x192) t = kT256x256;
   if (dtype == NKL_F16)
-    launch_dma<f16, f16, true>(t, a, 1, st);
+    launch_dma_cols<f16, f16, true>(t, a, 1, true, st);
   else
-    launch_dma<bf16, bf16, true>(t, a, 1, st);
+    launch_dma_cols<bf16, bf16, true>(t, a, 1, true, st);
   return check_launch("nkl_gemm_swiglu");
 }
 
