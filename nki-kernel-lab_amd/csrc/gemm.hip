@@ -799,59 +799,68 @@ static double round_step_us(DmaTile t) {
 }
 
 // Column split of a launch whose 256-row tiles leave a partial last round:
-// the columns of the whole rounds go to a first launch with that tile, the
-// rest to a second launch with the tile chosen for them alone (2048 x 11264
-// at 256 x 256: 256 tiles, then 96 -- instead, 256 tiles over the first 8192
-// columns and 192 tiles of 256 x 128 over the last 3072).  n1 = 0: no split.
-struct ColSplit {
+// the columns of the whole rounds go to a first launch, the rest to a second
+// launch with the tile chosen for them alone (2048 x 11264: 352 tiles of
+// 256 x 256 make a round and then 96 -- instead, 256 such tiles over the first
+// 8192 columns and 192 tiles of 256 x 128 over the last 3072).  The plan is
+// the cheapest, at the round times above plus 2 us for a second launch, of
+// the chosen tile over all columns and the column splits of the 256-row
+// tiles.  n1 = 0: one launch with t1.  swiglu: the gate/up GEMM, whose
+// wavefronts own 64 columns (no 256 x 192 tile).
+struct TilePlan {
+  DmaTile t1;
   int n1;
   DmaTile t2;
 };
-static ColSplit col_split(const GemmArgs& a, DmaTile t, int batch, bool swiglu) {
-  ColSplit cs{0, t};
-  int bm, bn;
-  tile_dims(t, bm, bn);
-  if (batch != 1 || forced_tile() >= 0 || bm != 256) return cs;
-  const long cus = gemm_cus(), tm = (a.M + 255) / 256, tiles = tm * ((a.N + bn - 1) / bn);
-  if (tiles <= cus || tiles % cus == 0 || tm > cus) return cs;
-  const long full_tn = (tiles / cus) * cus / tm;  // column tiles of the whole rounds
-  const long n1 = full_tn * bn;
-  if (n1 <= 0 || n1 >= a.N) return cs;
-  GemmArgs rest = a;
-  rest.N = (int)(a.N - n1);
-  DmaTile t2 = choose_tile(rest, 1);
-  if (swiglu && t2 == kT256x192) t2 = kT256x256;  // wavefronts own 64 columns
-  if (round_step_us(t2) == 0.0) return cs;
-  auto rounds = [&](long n) { return (double)((n + cus - 1) / cus); };
+static TilePlan plan_tiles(const GemmArgs& a, DmaTile t, int batch, bool swiglu) {
+  TilePlan best{t, 0, t};
+  if (batch != 1 || forced_tile() >= 0 || round_step_us(t) == 0.0) return best;
+  const long cus = gemm_cus();
   const double nk = (a.K + G_BK - 1) / G_BK;
-  const double whole = round_step_us(t) * rounds(tiles) * nk;
-  int bm2, bn2;
-  tile_dims(t2, bm2, bn2);
-  const double split = round_step_us(t) * rounds(tm * full_tn) * nk +
-                       round_step_us(t2) * rounds(tiles_of(rest, bm2, bn2, 1)) * nk + 2.0;  // + the second launch
-  if (split < whole) cs = ColSplit{(int)n1, t2};
-  return cs;
+  auto cost = [&](DmaTile x, int n) {
+    int bm, bn;
+    tile_dims(x, bm, bn);
+    const long tiles = (long)((a.M + bm - 1) / bm) * ((n + bn - 1) / bn);
+    return round_step_us(x) * (double)((tiles + cus - 1) / cus) * nk;
+  };
+  double cb = cost(t, a.N);
+  for (DmaTile x : {kT256x256, kT256x192, kT256x128}) {
+    if (swiglu && x == kT256x192) continue;
+    int bm, bn;
+    tile_dims(x, bm, bn);
+    const long tm = (a.M + 255) / 256, tiles = tm * ((a.N + bn - 1) / bn);
+    if (tiles <= cus || tiles % cus == 0 || tm > cus) continue;
+    const long n1 = (tiles / cus) * cus / tm * bn;  // the columns of the whole rounds
+    if (n1 <= 0 || n1 >= a.N) continue;
+    GemmArgs rest = a;
+    rest.N = (int)(a.N - n1);
+    DmaTile t2 = choose_tile(rest, 1);
+    if (swiglu && t2 == kT256x192) t2 = kT256x256;
+    if (round_step_us(t2) == 0.0) continue;
+    const double c = cost(x, (int)n1) + cost(t2, rest.N) + 2.0;
+    if (c < cb) cb = c, best = TilePlan{x, (int)n1, t2};
+  }
+  return best;
 }
 
-// launch_dma over a column split when col_split finds one (swiglu: the
-// gate/up GEMM, whose output has half the columns).
+// launch_dma after plan_tiles: one launch, or two over a column split.
 template <typename TI, typename TO, bool BT>
 static void launch_dma_cols(DmaTile t, const GemmArgs& g, int batch, bool swiglu, hipStream_t st) {
-  const ColSplit cs = col_split(g, t, batch, swiglu);
-  if (cs.n1 == 0) {
-    launch_dma<TI, TO, BT>(t, g, batch, st);
+  const TilePlan pl = plan_tiles(g, t, batch, swiglu);
+  if (pl.n1 == 0) {
+    launch_dma<TI, TO, BT>(pl.t1, g, batch, st);
     return;
   }
   GemmArgs g1 = g, g2 = g;
-  g1.N = cs.n1;
-  g2.N = g.N - cs.n1;
+  g1.N = pl.n1;
+  g2.N = g.N - pl.n1;
   const uint16_t* B = static_cast<const uint16_t*>(g.B);
-  g2.B = BT ? B + (long)cs.n1 * g.ldb : B + cs.n1;
-  const long coff = swiglu ? cs.n1 / 2 : cs.n1;
+  g2.B = BT ? B + (long)pl.n1 * g.ldb : B + pl.n1;
+  const long coff = swiglu ? pl.n1 / 2 : pl.n1;
   g2.C = static_cast<TO*>(g.C) + coff;
   if (g.R) g2.R = static_cast<const TO*>(g.R) + coff;
-  launch_dma<TI, TO, BT>(t, g1, 1, st);
-  launch_dma<TI, TO, BT>(cs.t2, g2, 1, st);
+  launch_dma<TI, TO, BT>(pl.t1, g1, 1, st);
+  launch_dma<TI, TO, BT>(pl.t2, g2, 1, st);
 }
 
 template <typename T, typename TO, bool BT>

@@ -172,6 +172,42 @@ def test_large_tile_gemms_with_ragged_edges(rng, M, K, N, layout):
     assert_within_bf16_ulps(_np(c), ref, 1, floor=2e-3)
 
 
+@pytest.mark.parametrize("M,K,N", [(2048, 2048, 11264), (3000, 1024, 7000), (2000, 512, 11000)])
+@pytest.mark.parametrize("layout", ["nt", "nn"])
+@pytest.mark.parametrize("out_dt", [torch.bfloat16, torch.float32])
+def test_column_split_matches_column_slices(rng, M, K, N, layout, out_dt):
+    """Shapes whose 256-row tiles leave a partial last round run as two
+    launches over column ranges (2048 x 11264: 256 x 256 tiles over the first
+    8192 columns, 256 x 128 over the rest).  Every column equals, bit for
+    bit, what a GEMM over a slice of the columns computes, residual included,
+    and is within one bf16 ulp of the float64 product."""
+    from nkilab import ops
+
+    a = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).to(torch.bfloat16).cuda()
+    b = torch.from_numpy(rng.standard_normal((N, K) if layout == "nt" else (K, N)).astype(np.float32))
+    b = b.to(torch.bfloat16).cuda()
+    r = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float32)).to(out_dt).cuda()
+
+    def run(bm, c, res):
+        return ops.linear_into(a, bm, c, residual=res) if layout == "nt" else ops.gemm_into(a, bm, c, residual=res)
+
+    c = torch.empty((M, N), dtype=out_dt, device="cuda")
+    run(b, c, r)
+    # slices of 2048 columns: their GEMMs take one-K-group tiles too (fewer
+    # columns would give the small two-K-group tiles another sum order)
+    for lo, hi in [(0, 2048), (N // 2 - 1088, N // 2 + 960), (N - 2048, N)]:
+        bs = b[lo:hi] if layout == "nt" else b[:, lo:hi]
+        cs = torch.empty((M, hi - lo), dtype=out_dt, device="cuda")
+        run(bs, cs, r[:, lo:hi])
+        assert torch.equal(c[:, lo:hi], cs), (lo, hi)
+        bt = bs.double().cpu() if layout == "nn" else bs.double().cpu().t()
+        ref = (a[:512].double().cpu() @ bt + r[:512, lo:hi].double().cpu()).numpy()  # first 512 rows
+        if out_dt == torch.bfloat16:
+            assert_within_bf16_ulps(_np(cs[:512]), ref, 1, floor=2e-3)
+        else:
+            assert rel_err(_np(cs[:512]), ref) < 1e-5
+
+
 @pytest.mark.parametrize("M,K,N", [(2048, 2048, 5632), (300, 256, 96), (64, 128, 32), (1, 64, 64), (513, 384, 704)])
 def test_gemm_swiglu_equals_gate_up_then_swiglu(rng, M, K, N):
     """The fused gate/up GEMM with SwiGLU in its epilogue is bit-identical to
