@@ -504,6 +504,10 @@ PMC_WORKLOADS = {"attention": "flash", "attention_1x4096": "flash", "attention_3
 DECODER_GEMMS = {"gemm_qkv": (2048, 6144, 2048), "gemm_wo": (2048, 2048, 2048), "gemm_gate_up": (2048, 11264, 2048),
                  "gemm_down": (2048, 2048, 5632)}
 PMC_REPS = 8
+# Calls of the workload in one counter pass where not PMC_REPS.  Counters are
+# reported per call: a call can be several dispatches (the decoder forward;
+# the gate/up GEMM split over two column ranges).
+PMC_CALLS = {"attention_32x16384": 2, "decoder": 2}
 
 
 def pmc_pass(workload: str) -> None:
@@ -632,7 +636,6 @@ def parse_counters(out_dir: str, only: list[str] | None = None) -> dict:
         for tag in ("fetch", "write", "mfma"):
             per = {}  # counter -> (sum over the workload's dispatches, dispatches)
             calib = {}
-            disp = set()
             for name, ctr, val, did in _rows(csv_of(wl, tag)):
                 if "neg_kernel" in name:
                     calib[ctr] = calib.get(ctr, 0.0) + val / 3.0
@@ -643,9 +646,7 @@ def parse_counters(out_dir: str, only: list[str] | None = None) -> dict:
                     continue  # torch's own fills and copies around the block
                 t, n = per.get(ctr, (0.0, 0))
                 per[ctr] = (t + val, n)
-                disp.add(did)
-            ndisp = max(len(disp), 1)
-            launches = ndisp if pat else 2  # the decoder pass runs the block twice
+            launches = PMC_CALLS.get(wl, PMC_REPS)
             if tag == "fetch":
                 f = calib["FETCH_SIZE"] * 1024 / COPY_BYTES
                 ent["read_bytes"] = round(per["FETCH_SIZE"][0] / launches * 1024 / f)
