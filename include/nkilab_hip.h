@@ -70,6 +70,9 @@ const char* nkl_last_error_string(void);
  * F16 operands take the LDS-DMA kernel only: 16-byte aligned A and B, K,
  * lda, ldb (and N when b_trans == 0) multiples of 8, operands under 2 GiB;
  * other F16 shapes return NKL_EDTYPE.
+ * The work is enqueued on `stream` as one kernel launch, or as two over
+ * column ranges when the large tiles would leave a partial last round of
+ * workgroups; nothing is allocated, and the call can be captured in a graph.
  */
 int nkl_gemm(const void* A, const void* B, void* C, const void* R,
              int M, int N, int K, long lda, long ldb, long ldc, long ldr,
@@ -90,7 +93,8 @@ int nkl_gemm(const void* A, const void* B, void* C, const void* R,
  * N must be a multiple of 32; pointers 16-byte aligned; K, lda, ldb, ldc
  * multiples of 8.  The gate and up accumulators are rounded to dtype before
  * silu(gate) * up is formed in fp32 and rounded once, so C equals what two
- * dtype GEMMs followed by a SwiGLU in dtype produce.
+ * dtype GEMMs followed by a SwiGLU in dtype produce.  Like nkl_gemm, one or
+ * two kernel launches on `stream`.
  */
 int nkl_gemm_swiglu(const void* A, const void* Bgu, void* C, int M, int N,
                     int K, long lda, long ldb, long ldc, int dtype,
