@@ -210,10 +210,13 @@ int nkl_flash_attn_causal(const void* q, const void* k, const void* v,
  *     the first call; every call leaves them zero, so one zeroed array (of
  *     the largest size needed) can serve successive calls of any shape on
  *     one stream.  Calls that may overlap need separate arrays.
- * Both sizes are 0 for f32, and for bf16 shapes with at least as many query
- * blocks (H * ceil(S / 128)) as the GPU has CUs: those run as
- * nkl_flash_attn_causal does and ignore the scratch.  Same reference lines as
- * nkl_flash_attn_causal.
+ * Both sizes are 0 exactly when the schedule chosen for the shape is not the
+ * balanced one: f32, and the largest bf16 shapes (about 1024 key tiles of
+ * 128 queries per CU and up, e.g. 32 x 16384 on 256 CUs), which run as
+ * nkl_flash_attn_causal does and ignore the scratch.  Most shapes, including
+ * ones with more query blocks than CUs (16 x 2048), need it: query the two
+ * sizes for every shape rather than predicting them.  Same reference lines
+ * as nkl_flash_attn_causal.
  */
 size_t nkl_flash_attn_causal_workspace_bytes(int H, int S, int d, int dtype);
 size_t nkl_flash_attn_causal_counter_bytes(int H, int S, int dtype);

@@ -193,8 +193,10 @@ def test_column_split_matches_column_slices(rng, M, K, N, layout, out_dt):
 
     c = torch.empty((M, N), dtype=out_dt, device="cuda")
     run(b, c, r)
-    # slices of 2048 columns: their GEMMs take one-K-group tiles too (fewer
-    # columns would give the small two-K-group tiles another sum order)
+    # slices of 2048 columns: their GEMMs take one-K-group tiles too, or the
+    # element kernel for a [K, N] slice that is not 16-byte aligned, both
+    # summing K in the same order (fewer columns would give the small
+    # two-K-group tiles another sum order)
     for lo, hi in [(0, 2048), (N // 2 - 1088, N // 2 + 960), (N - 2048, N)]:
         bs = b[lo:hi] if layout == "nt" else b[:, lo:hi]
         cs = torch.empty((M, hi - lo), dtype=out_dt, device="cuda")

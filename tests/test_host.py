@@ -70,6 +70,9 @@ def test_flash_scratch_sizes():
     assert L.nkl_flash_attn_causal_workspace_bytes(8, 2048, 128, 1) > 0
     assert L.nkl_flash_attn_causal_counter_bytes(8, 2048, 1) == 8 * 32 * 4
     assert L.nkl_flash_attn_causal_counter_bytes(1, 4096, 1) == 64 * 4
+    # more query blocks (256) than CUs, still the balanced schedule: scratch needed
+    assert L.nkl_flash_attn_causal_workspace_bytes(16, 2048, 128, 1) > 0
+    assert L.nkl_flash_attn_causal_counter_bytes(16, 2048, 1) == 16 * 32 * 4
     assert L.nkl_flash_attn_causal_workspace_bytes(32, 16384, 128, 1) == 0
     assert L.nkl_flash_attn_causal_counter_bytes(32, 16384, 1) == 0
     assert L.nkl_flash_attn_causal_workspace_bytes(8, 2048, 128, 0) == 0  # f32 needs none
