@@ -18,6 +18,7 @@
 // kernel's 16-byte loads cannot address): each wavefront computes one 32x32
 // tile of C reading its operands straight from global memory at every K step
 // -- no on-chip reuse, like the reference's matmul_naive.
+#include <atomic>
 #include <cstdlib>
 #include <cstring>
 #include <type_traits>
@@ -765,17 +766,18 @@ static DmaTile choose_tile(const GemmArgs& a, int batch) {
   return kT64x64K2;
 }
 
-// CUs of the current device (256 on MI355X), read once per device.
+// CUs of the current device (256 on MI355X), read once per device (threads
+// that race to read it store the same value).
 static int gemm_cus() {
-  static int cus[64] = {};
+  static std::atomic<int> cus[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cus[dev]) {
-    int n = 0;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cus[dev] = n;
+    cus[dev].store(n, std::memory_order_relaxed);
   }
-  return cus[dev];
+  return n;
 }
 
 // Rows and columns of a tile.
