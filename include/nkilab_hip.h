@@ -67,9 +67,10 @@ const char* nkl_last_error_string(void);
  *      NULL for none.
  * Products accumulate in fp32; C is rounded once (round-to-nearest-even) to
  * dtype_out.  dtype_in in {F32, BF16, F16}; dtype_out in {F32, dtype_in}.
- * F16 operands take the LDS-DMA kernel only: 16-byte aligned A and B, K,
- * lda, ldb (and N when b_trans == 0) multiples of 8, operands under 2 GiB;
- * other F16 shapes return NKL_EDTYPE.
+ * BF16 and F16 operands take the LDS-DMA kernel when A and B are 16-byte
+ * aligned, K, lda, ldb (and N when b_trans == 0) are multiples of 8 and the
+ * operands are under 2 GiB; other shapes, and variant NKL_GEMM_NAIVE, take a
+ * one-tile-per-wavefront kernel (the same fp32 accumulation).
  * The work is enqueued on `stream` as one kernel launch, or as two over
  * column ranges when the large tiles would leave a partial last round of
  * workgroups; nothing is allocated, and the call can be captured in a graph.
@@ -151,7 +152,8 @@ int nkl_rmsnorm_ex(const void* x, const void* w, void* y, int rows, int cols,
                    int dtype_out, void* stream);
 
 /*
- * y = silu(g) * u, element-wise over n contiguous elements.
+ * y = silu(g) * u, element-wise over n contiguous elements (fp32, bf16 or
+ * fp16; silu and the product in fp32, one rounding).
  * Replaces nkilab/kernels/norm.py:121 (swiglu_fused), nkilab/ops.py:65.
  */
 int nkl_swiglu(const void* g, const void* u, void* y, long n, int dtype,
@@ -187,11 +189,12 @@ int nkl_stream_copy(const void* x, void* y, long nbytes, void* stream);
  * Replaces nkilab/kernels/attention.py:280 (flash_attention_pipelined, the
  * default of nkilab/ops.py:77) and its numerically identical siblings
  * attention.py:155, :179, :249; called from nkilab/ops.py:90.
- * q, k, v, o: [H, S, d] with element strides (*_sh between heads, *_ss between
- * positions) and unit stride along d; any S >= 1, 1 <= d <= 128.
+ * q, k, v, o: [H, S, d] with element strides (*_sh between heads, at most
+ * 2^24; *_ss between positions, at most 2^21) and unit stride along d; any
+ * S >= 1, 1 <= d <= 128.
  * bf16: P is rounded to bf16 before P.V, statistics and O accumulate in fp32,
  * O is rounded once.  f16: the same with fp16 operands, P and O (the teams
- * kernel for every shape).  f32: everything in fp32.
+ * or key-split kernel).  f32: everything in fp32.
  */
 int nkl_flash_attn_causal(const void* q, const void* k, const void* v,
                           void* o, int H, int S, int d, long q_sh, long q_ss,
@@ -234,7 +237,10 @@ int nkl_flash_attn_causal_ws(const void* q, const void* k, const void* v,
  *   kernel:   0 teams, 1 one wavefront per SIMD (32 queries), 2 (64 queries,
  *             2 wavefronts), 3 (64 queries, 4 wavefronts), 4 4-wavefront
  *             teams, 5 one-wavefront kernel at two per SIMD, 6 the
- *             64-key-tile kernel (d > 64 only);
+ *             64-key-tile kernel, 7 the same with its two key-half
+ *             wavefronts half an iteration apart, 8 the key-split kernel
+ *             (64-query blocks, four wavefronts that each take every
+ *             fourth key tile; kernels 6-8 for 64 < d <= 128 only);
  *   schedule: 0 block, 1 balanced (needs the scratch of
  *             nkl_flash_attn_causal_ws), 2 pairs;
  *   qb:       64 or 128 queries per block (kernels 0 and 4);
@@ -245,6 +251,17 @@ int nkl_flash_attn_causal_ws(const void* q, const void* k, const void* v,
  * while another thread sizes or launches attention.
  */
 int nkl_flash_attn_configure(int kernel, int schedule, int qb, int cpb);
+
+/*
+ * Test and tuning control, process-wide, of the balanced schedule: the poll
+ * budget (0 .. 2^20, -1 for the default 4096) of the workgroup that merges a
+ * split query block while it waits for the block's other parts.  Past the
+ * budget it stores its own state and arrives like the others, and the last to
+ * arrive merges; the parts are folded in the same order either way, so every
+ * budget gives the same bits.  No counterpart in the reference (its kernels
+ * have no split blocks).
+ */
+int nkl_flash_attn_configure_polls(int polls);
 
 /*
  * Unfused causal attention: scores (fp32, [H, S, S]) and probabilities
@@ -305,7 +322,8 @@ int nkl_flash_attn_causal_noalloc(const void* q, const void* k, const void* v,
  * Rotary position embedding, rotate-half layout (RoFormer, as GPT-NeoX and
  * Llama apply it): for each head h and row s of x [H, S, d] (strides x_sh,
  * x_ss; d even), element i < d/2 and element i + d/2 rotate by the angle
- * (pos0 + s) * base^(-2 i / d).  fp32 arithmetic, one rounding per output;
+ * (pos0 + s) * base^(-2 i / d).  fp32, bf16 or fp16 x and y; fp32
+ * arithmetic, one rounding per output;
  * y may be x (in place).  No counterpart in the reference (README.md:89 lists
  * rotary embeddings as not implemented); applied to q and k before attention.
  */

@@ -37,7 +37,15 @@ struct Work;
 // (matrix-core work of one beside vector work of the other).
 void launch_flash_fwd(const AttnArgs& a, const fsched::Work& w, bool pingpong, hipStream_t st);
 size_t flash_fwd_part_bytes();
+// The key-split kernel (flash_ks.hip) for 64 < d <= 128: launch over a
+// planned Work (64-query blocks, 32-key tiles, four wavefronts that each take
+// every fourth tile of a segment), and the bytes of one part's state of a
+// block (the workspace holds two per range).
+void launch_flash_ks(const AttnArgs& a, const fsched::Work& w, hipStream_t st);
+size_t flash_ks_part_bytes();
 // Process-wide kernel / schedule / block / start-cost overrides (-1: automatic).
 int flash_bf16_configure(int kern, int sched, int qb, int cpb);
+// Process-wide poll budget of the workgroup that merges a split block (-1: 4096).
+int flash_bf16_configure_polls(int polls);
 
 }  // namespace nkl

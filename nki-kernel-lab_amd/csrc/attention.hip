@@ -332,6 +332,8 @@ static int flash_f32_dispatch(const AttnArgs& a, hipStream_t st) {
 
 using namespace nkl;
 
+constexpr long kMaxRowStride = 1L << 21;
+
 static int check_attn(const char* fn, const void* q, const void* k, const void* v, const void* o, int H, int S,
                       int d, int dtype, const long* strides) {
   if (H < 0 || S < 0) return set_error(NKL_EINVAL, "%s: negative shape H=%d S=%d", fn, H, S);
@@ -343,11 +345,17 @@ static int check_attn(const char* fn, const void* q, const void* k, const void* 
     return set_error(NKL_EINVAL, "%s: d=%d must be a multiple of %d (pad the head dim on the host)", fn, d, E);
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
     return set_error(NKL_EINVAL, "%s: q/k/v/o must be 16-byte aligned", fn);
+  if (H > 0 && S > 0 && (!q || !k || !v || !o)) return set_error(NKL_EINVAL, "%s: null q/k/v/o", fn);
+  // Head strides (even entries) up to 2^24 elements; row strides (odd) up to
+  // 2^21, so that the kernels' 32-bit byte offsets within a block of up to 256
+  // rows stay below 2^30 -- the offset at which a copy of a chunk past d reads
+  // zeros from outside every buffer.
   for (int i = 0; i < 8; ++i) {
+    const long lim = i % 2 ? kMaxRowStride : 1L << 24;
     if (strides[i] % E != 0)
       return set_error(NKL_EINVAL, "%s: stride %ld is not a multiple of %d elements", fn, strides[i], E);
-    if (strides[i] < 0 || strides[i] > (1L << 24))
-      return set_error(NKL_EINVAL, "%s: stride %ld outside [0, 2^24]", fn, strides[i]);
+    if (strides[i] < 0 || strides[i] > lim)
+      return set_error(NKL_EINVAL, "%s: %s stride %ld outside [0, %ld]", fn, i % 2 ? "row" : "head", strides[i], lim);
   }
   return NKL_OK;
 }
@@ -478,6 +486,8 @@ extern "C" int nkl_flash_attn_configure(int kernel, int schedule, int qb, int cp
   return flash_bf16_configure(kernel, schedule, qb, cpb);
 }
 
+extern "C" int nkl_flash_attn_configure_polls(int polls) { return flash_bf16_configure_polls(polls); }
+
 extern "C" size_t nkl_attention_naive_workspace_bytes(int H, int S, int dtype) {
   if (H <= 0 || S <= 0) return 0;
   const size_t n = (size_t)H * S * S;
@@ -488,7 +498,6 @@ extern "C" size_t nkl_attention_naive_workspace_bytes(int H, int S, int dtype) {
 static int naive_entry(const char* fn, const void* q, const void* k, const void* v, void* o, void* workspace,
                        size_t workspace_bytes, int H, int Hkv, int S, int d, const long* st8, float scale, int dtype,
                        void* stream) {
-  if (dtype == NKL_F16) return set_error(NKL_EDTYPE, "%s: the naive attention takes fp32 or bf16", fn);
   int rc = check_attn(fn, q, k, v, o, H, S, d, dtype, st8);
   if (rc) return rc;
   if (Hkv < 1 || H % Hkv != 0)
@@ -519,6 +528,8 @@ static int naive_entry(const char* fn, const void* q, const void* k, const void*
   const dim3 grid((unsigned)(((long)H * S + 3) / 4)), block(256);
   if (dtype == NKL_BF16)
     masked_softmax_kernel<bf16><<<grid, block, 0, st>>>(sc, reinterpret_cast<bf16*>(pr), H, S, scale);
+  else if (dtype == NKL_F16)
+    masked_softmax_kernel<f16><<<grid, block, 0, st>>>(sc, reinterpret_cast<f16*>(pr), H, S, scale);
   else
     masked_softmax_kernel<float><<<grid, block, 0, st>>>(sc, reinterpret_cast<float*>(pr), H, S, scale);
   rc = check_launch(fn);

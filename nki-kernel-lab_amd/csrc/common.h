@@ -236,6 +236,15 @@ struct Mfma32<bf16> {
   }
 };
 template <>
+struct Mfma32<f16> {
+  static constexpr int KPER = 8;
+  static constexpr int MK = 16;
+  typedef f16x8 frag;
+  static __device__ __forceinline__ floatx16 mma(frag a, frag b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
 struct Mfma32<float> {
   static constexpr int KPER = 1;
   static constexpr int MK = 2;

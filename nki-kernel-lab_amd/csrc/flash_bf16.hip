@@ -541,7 +541,7 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
       // The holder of the block's last range waits for the other parts to
       // arrive instead of storing its own state (see await_parts).
       const int vl = vf + nparts - 1;
-      if (vidx == vl) await_parts(&w.count[hh * w.nqb + b], nparts, arrival);
+      if (vidx == vl) await_parts(&w.count[hh * w.nqb + b], nparts, w.polls, arrival);
       if (vidx != vl || arrival != nparts - 1) {
         if (keeps) {
 #pragma unroll
@@ -1039,7 +1039,7 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
       };
       const int slot = range_start(vidx, w) >= bstart ? 0 : 1;
       const int vl = vf + nparts - 1;
-      if (vidx == vl) await_parts(&w.count[hh * w.nqb + b], nparts, arrival);
+      if (vidx == vl) await_parts(&w.count[hh * w.nqb + b], nparts, w.polls, arrival);
       const bool stored = vidx != vl || arrival != nparts - 1;
 #pragma unroll
       for (int hq = 0; hq < QH && stored; ++hq) {
@@ -1133,16 +1133,17 @@ int cu_count() {
 // (256 registers each, two independent workgroups per CU); or the
 // 64-key-tile kernel of flash_fwd.hip (kFwd: 128-query blocks, two
 // wavefronts per SIMD splitting each tile's keys, LDS-DMA stages).
-enum Kern { kTeams = 0, kW32x4 = 1, kW64x2 = 2, kW64x4 = 3, kTeams4 = 4, kW32x4x2 = 5, kFwd = 6, kFwdPP = 7 };
+enum Kern { kTeams = 0, kW32x4 = 1, kW64x2 = 2, kW64x4 = 3, kTeams4 = 4, kW32x4x2 = 5, kFwd = 6, kFwdPP = 7, kKS = 8 };
 
 // Launch-configuration overrides (-1: the automatic choice), process-wide:
 // read from the environment once, at first use -- NKL_FLASH_SCHEDULE=
 // block|pairs|balanced, NKL_FLASH_QB=64|128,
-// NKL_FLASH_KERNEL=teams|teams4|w1|w1o2|w64|w64x4|fwd, NKL_FLASH_CPB=<units>
+// NKL_FLASH_KERNEL=teams|teams4|w1|w1o2|w64|w64x4|fwd|pp|ks, NKL_FLASH_CPB=<units>
 // -- or set by nkl_flash_attn_configure() (tests, tuning), so that a
 // workspace sized by one call fits the launch of the next.
 struct Overrides {
   int sched = -1, qb = -1, kern = -1, cpb = -1;
+  int polls = -1;  // the merging workgroup's poll budget (-1: 4096)
 };
 Overrides& overrides() {
   static Overrides o = [] {
@@ -1165,6 +1166,7 @@ Overrides& overrides() {
       if (!strcmp(f, "w64x4")) r.kern = kW64x4;
       if (!strcmp(f, "fwd")) r.kern = kFwd;
       if (!strcmp(f, "pp")) r.kern = kFwdPP;
+      if (!strcmp(f, "ks")) r.kern = kKS;
     }
     if (const char* f = getenv("NKL_FLASH_CPB")) r.cpb = min(max(atoi(f), 0), 4096);
     return r;
@@ -1175,7 +1177,7 @@ Overrides& overrides() {
 }  // namespace
 
 int flash_bf16_configure(int kern, int sched, int qb, int cpb) {
-  if (kern < -1 || kern > kFwdPP || sched < -1 || sched > kPairs || (qb != -1 && qb != 64 && qb != 128) || cpb < -1 ||
+  if (kern < -1 || kern > kKS || sched < -1 || sched > kPairs || (qb != -1 && qb != 64 && qb != 128) || cpb < -1 ||
       cpb > 4096)
     return set_error(NKL_EINVAL, "nkl_flash_attn_configure: kernel %d, schedule %d, qb %d, cpb %d out of range", kern,
                      sched, qb, cpb);
@@ -1184,6 +1186,13 @@ int flash_bf16_configure(int kern, int sched, int qb, int cpb) {
   o.sched = sched;
   o.qb = qb;
   o.cpb = cpb;
+  return NKL_OK;
+}
+
+int flash_bf16_configure_polls(int polls) {
+  if (polls < -1 || polls > (1 << 20))
+    return set_error(NKL_EINVAL, "nkl_flash_attn_configure_polls: %d outside [-1, 2^20]", polls);
+  overrides().polls = polls;
   return NKL_OK;
 }
 
@@ -1214,6 +1223,7 @@ Work plan(int H, int S, Config cfg) {
   w.units = (long)H * w.units_head;
   w.sched = cfg.sched;
   w.paired = cfg.sched != kBlock;
+  w.polls = overrides().polls < 0 ? 4096 : overrides().polls;
   if (cfg.sched == kBalanced) {
     // As many workgroups as are resident at once, and no range shorter than
     // kMinUnits: a short range spends most of its time filling the pipeline,
@@ -1235,7 +1245,7 @@ Work plan(int H, int S, Config cfg) {
     const bool pipelined = cfg.kern == kW32x4 || cfg.kern == kW64x2 || cfg.kern == kW64x4 || cfg.kern == kW32x4x2;
     const long nblocks = (long)H * w.nqb;
     const bool few = nblocks < w.grid;
-    int cpb = fwd ? (few ? 4 : 2) : pipelined ? 2 : cfg.qb == 64 ? (few ? 18 : 10) : (few ? 6 : 4);
+    int cpb = fwd ? (few ? 4 : 2) : pipelined ? 2 : cfg.kern == kKS ? (few ? 8 : 6) : cfg.qb == 64 ? (few ? 18 : 10) : (few ? 6 : 4);
     if (overrides().cpb >= 0) cpb = overrides().cpb;
     while (cpb > 0 && (w.units + nblocks * cpb) / w.grid < cpb + 1) --cpb;
     w.cpb = cpb < 0 ? 0 : cpb;
@@ -1292,10 +1302,12 @@ Config choose(int H, int S, int d, bool f16) {
   if (ov.qb >= 0) cfg.qb = ov.qb;
   if (ov.kern >= 0) cfg.kern = ov.kern;
   if (d <= 64 && cfg.kern != kTeams4) cfg.kern = kTeams;
-  if (f16 && cfg.kern != kTeams4) cfg.kern = kTeams;  // fp16: the teams kernels only
+  if (f16 && cfg.kern != kTeams4 && cfg.kern != kKS) cfg.kern = kTeams;  // fp16: the teams and key-split kernels
   if (cfg.kern == kW32x4 || cfg.kern == kW64x2 || cfg.kern == kW32x4x2 || cfg.kern == kFwd || cfg.kern == kFwdPP)
     cfg.qb = 128;
   if (cfg.kern == kW64x4) cfg.qb = 256;
+  if (cfg.kern == kKS && (d <= 64 || d > 128)) cfg.kern = kTeams;  // the key-split kernel: 64 < d <= 128
+  if (cfg.kern == kKS) cfg.qb = 64;
   return cfg;
 }
 
@@ -1309,6 +1321,7 @@ size_t part_floats(int qb) {
 
 size_t part_floats_for(int d, const Config& cfg) {
   if (cfg.kern == kFwd || cfg.kern == kFwdPP) return flash_fwd_part_bytes() / 4;
+  if (cfg.kern == kKS) return flash_ks_part_bytes() / 4;
   return d <= 32 ? part_floats<32>(cfg.qb) : d <= 64 ? part_floats<64>(cfg.qb) : part_floats<128>(cfg.qb);
 }
 
@@ -1359,6 +1372,10 @@ size_t flash_bf16_counter_bytes(int H, int S) {
 int flash_bf16_launch(const AttnArgs& a, void* workspace, size_t workspace_bytes, int* counters,
                       size_t counter_bytes, hipStream_t st) {
   Config cfg = choose(a.H, a.S, a.d, a.f16 != 0);
+  // The key-split kernel copies K and V rows with one stride; other layouts
+  // take the teams kernel over the same 64-query blocks (whose partial states
+  // have the same size).
+  if (cfg.kern == kKS && (a.k_ss != a.v_ss || !(a.c > 0.f))) cfg.kern = kTeams;
   if (cfg.sched == kBalanced && !workspace) cfg.sched = kPairs;  // the plain entry point: no scratch
   Work w = plan(a.H, a.S, cfg);
   if (cfg.sched == kBalanced) {
@@ -1374,6 +1391,11 @@ int flash_bf16_launch(const AttnArgs& a, void* workspace, size_t workspace_bytes
   }
   if (cfg.kern == kFwd || cfg.kern == kFwdPP) {
     launch_flash_fwd(a, w, cfg.kern == kFwdPP, st);
+    return check_launch("nkl_flash_attn_causal");
+  }
+  if (cfg.kern == kKS && w.fast) {
+    w.dv_group = make_div32((unsigned)a.group);
+    launch_flash_ks(a, w, st);
     return check_launch("nkl_flash_attn_causal");
   }
   if (cfg.kern == kW32x4 || cfg.kern == kW64x2 || cfg.kern == kW64x4 || cfg.kern == kW32x4x2) {

@@ -746,7 +746,7 @@ void flash_fwd_kernel(AttnArgs p, Work w) {
       // The holder of the block's last range merges: it waits for the other
       // parts' arrivals instead of storing its own state (await_parts).
       const int vl = vf + nparts - 1;
-      if (vidx == vl) await_parts(&w.count[hh * w.nqb + b], nparts, arrival);
+      if (vidx == vl) await_parts(&w.count[hh * w.nqb + b], nparts, w.polls, arrival);
       if (vidx != vl || arrival != nparts - 1) {
         const int base = pbase(vidx);
 #pragma unroll

@@ -80,12 +80,14 @@ struct Work {
   float* part;      // balanced: partial states
   int part_bytes;   // balanced: bytes of part
   int* count;       // balanced: arrival counters [H][nqb], zero between calls
+  int polls;        // balanced: poll budget of the workgroup that merges a split block (await_parts)
   // Magic divisors of the launch constants below, valid when fast is set
   // (every dividend of the schedule arithmetic fits in 32 bits): units_head,
   // the pair span tpb (nqb + 1), its cost tpb (nqb + 1) + 2 cpb, the head
   // cost, grid and cost.
   int fast;
   Div32 dv_units_head, dv_full, dv_fcost, dv_head_cost, dv_grid, dv_cost;
+  Div32 dv_group;  // query heads per K/V head (set at launch)
 };
 
 // a / b for 0 <= a, 0 < b: a 32-bit division when both fit (every realistic
@@ -206,6 +208,28 @@ __device__ __forceinline__ int wg_range(const Work& w, int H, long& u0, long& u1
   return vidx;
 }
 
+// wg_range with 32-bit arithmetic throughout (Work::fast must hold): no
+// 64-bit paths, whose division set-up the compiler would otherwise hoist to
+// the kernel's start.
+__device__ __forceinline__ int wg_range_fast(const Work& w, int H, int& u0, int& u1) {
+  int vidx = blockIdx.x;
+  if (w.sched == kBalanced) {
+    if (w.grid % 8 == 0) vidx = (blockIdx.x % 8) * (w.grid / 8) + blockIdx.x / 8;
+    u0 = range_start_t<int>(vidx, w);
+    u1 = range_start_t<int>(vidx + 1, w);
+  } else if (w.sched == kPairs) {
+    const int hh = blockIdx.x % H, k = blockIdx.x / H;
+    u0 = hh * (int)w.units_head + pair_before<int>(k, w);
+    u1 = 2 * k + 2 <= w.nqb ? hh * (int)w.units_head + pair_before<int>(k + 1, w) : (hh + 1) * (int)w.units_head;
+  } else {
+    const int hh = blockIdx.x % H;
+    const int b = w.nqb - 1 - blockIdx.x / H;  // heaviest first
+    u0 = hh * (int)w.units_head + plain_before<int>(b, w);
+    u1 = u0 + block_tiles(b, w);
+  }
+  return vidx;
+}
+
 // A segment: head hh, query block b, tiles [t0, t1) of the block's nt tiles,
 // whose first unit is bstart.
 struct Seg {
@@ -261,13 +285,15 @@ __host__ __device__ __forceinline__ Seg decode_seg(long u, long u0, const Work& 
 // ranges -- have stored their states and arrived, so rather than store its own
 // state and arrive it polls the block's counter until the other nparts - 1
 // have arrived (their arrivals never reach nparts - 1 without it) and sets
-// `arrival` to nparts - 1.  The poll is bounded (4096 polls, each followed by
-// ~512 cycles of sleep: ~1 ms); past that `arrival` is -1 and the workgroup
-// stores its state and arrives like the others, the last of which merges.
-__device__ __forceinline__ void await_parts(int* count, int nparts, int& arrival) {
+// `arrival` to nparts - 1.  The poll is bounded (Work::polls polls, by
+// default 4096, each followed by ~512 cycles of sleep: ~1 ms); past that
+// `arrival` is -1 and the workgroup stores its state and arrives like the
+// others, the last of which merges.  Either way the states are folded in the
+// same order, so the result does not depend on which workgroup merges.
+__device__ __forceinline__ void await_parts(int* count, int nparts, int polls, int& arrival) {
   if (threadIdx.x == 0) {
     int n = 0;
-    for (int it = 0; it < 4096; ++it) {
+    for (int it = 0; it < polls; ++it) {
       n = __hip_atomic_load(count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (n == nparts - 1) break;
       __builtin_amdgcn_s_sleep(8);

@@ -872,12 +872,16 @@ static int gemm_dispatch(const GemmArgs& a, int batch, int variant, hipStream_t 
                    a.sA % E == 0 && a.sB % E == 0 && (BT || a.N % E == 0);
   constexpr bool half = std::is_same<T, f16>::value;
   if constexpr (half) {
-    // fp16 operands: the LDS-DMA kernel only.
+    // fp16 operands: the LDS-DMA kernel, or for the naive variant, unaligned
+    // operands, K or leading dimensions off a multiple of 8 and operands over
+    // 2 GiB, the one-tile-per-wavefront kernel.
     const long a_bytes = 2L * ((long)(a.M - 1) * a.lda + a.K), b_bytes = BT ? 2L * ((long)(a.N - 1) * a.ldb + a.K)
                                                                         : 2L * ((long)(a.K - 1) * a.ldb + a.N);
-    if (variant == NKL_GEMM_NAIVE || !vec || a_bytes >= (1L << 31) || b_bytes >= (1L << 31))
-      return set_error(NKL_EDTYPE, "nkl_gemm: fp16 operands need the blocked variant, 16-byte aligned operands with K "
-                       "and leading dimensions multiples of 8, and operands under 2 GiB");
+    if (variant == NKL_GEMM_NAIVE || !vec || a_bytes >= (1L << 31) || b_bytes >= (1L << 31)) {
+      const long tiles = (long)((a.M + 31) / 32) * ((a.N + 31) / 32);
+      gemm_naive_kernel<T, TO, BT><<<dim3((unsigned)((tiles + 3) / 4), 1, batch), dim3(256), 0, st>>>(a);
+      return check_launch("nkl_gemm(naive)");
+    }
     GemmArgs g = a;
     g.epi = staged_ok<TO>(a) ? kEpiStaged : kEpiElem;
     launch_dma_cols<f16, TO, BT>(choose_tile(a, batch), g, batch, false, st);

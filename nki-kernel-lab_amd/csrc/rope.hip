@@ -62,12 +62,14 @@ extern "C" int nkl_rope(const void* x, void* y, int H, int S, int d, long x_sh, 
   if (pos0 < 0 || (long)pos0 + S > (1L << 24))
     return set_error(NKL_EINVAL, "nkl_rope: positions [%d, %ld) outside [0, 2^24)", pos0, (long)pos0 + S);
   if (!(base > 1.0f) || !isfinite(base)) return set_error(NKL_EINVAL, "nkl_rope: base %g must be finite and > 1", base);
-  if (dtype != NKL_F32 && dtype != NKL_BF16) return set_error(NKL_EDTYPE, "nkl_rope: unsupported dtype %d", dtype);
+  if (dtype != NKL_F32 && dtype != NKL_BF16 && dtype != NKL_F16)
+    return set_error(NKL_EDTYPE, "nkl_rope: unsupported dtype %d", dtype);
   if (x_ss < d || y_ss < d) return set_error(NKL_EINVAL, "nkl_rope: row stride below d");
   if ((long)H * S * (d / 2) >= (1L << 31) * 256L) return set_error(NKL_EINVAL, "nkl_rope: tensor too large");
   if (H == 0 || S == 0 || d == 0) return NKL_OK;
   if (!x || !y) return set_error(NKL_EINVAL, "nkl_rope: null pointer");
   hipStream_t st = (hipStream_t)stream;
   if (dtype == NKL_F32) return rope_launch<float>(x, y, H, S, d, x_sh, x_ss, y_sh, y_ss, pos0, base, st);
+  if (dtype == NKL_F16) return rope_launch<f16>(x, y, H, S, d, x_sh, x_ss, y_sh, y_ss, pos0, base, st);
   return rope_launch<bf16>(x, y, H, S, d, x_sh, x_ss, y_sh, y_ss, pos0, base, st);
 }

@@ -487,6 +487,7 @@ extern "C" int nkl_swiglu(const void* g, const void* u, void* y, long n, int dty
   hipStream_t st = (hipStream_t)stream;
   if (dtype == NKL_F32) return swiglu_launch<float>(g, u, y, n, st);
   if (dtype == NKL_BF16) return swiglu_launch<bf16>(g, u, y, n, st);
+  if (dtype == NKL_F16) return swiglu_launch<f16>(g, u, y, n, st);
   return set_error(NKL_EDTYPE, "nkl_swiglu: unsupported dtype %d", dtype);
 }
 

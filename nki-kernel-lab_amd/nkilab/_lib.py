@@ -54,6 +54,7 @@ SIGNATURES = {
     "nkl_rope": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _c_long, _c_long, _c_long, _c_long, _c_int, _c_float,
                           _c_int, _vp]),
     "nkl_flash_attn_configure": (_c_int, [_c_int, _c_int, _c_int, _c_int]),
+    "nkl_flash_attn_configure_polls": (_c_int, [_c_int]),
     "nkl_attention_naive_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int]),
     "nkl_attention_naive": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_size, _c_int, _c_int, _c_int, _c_long, _c_long,
                                      _c_long, _c_long, _c_long, _c_long, _c_long, _c_long, _c_float, _c_int, _vp]),
@@ -88,7 +89,7 @@ def lib() -> ctypes.CDLL:
 
 
 # Codes of nkl_flash_attn_configure (include/nkilab_hip.h).
-FLASH_KERNELS = {"teams": 0, "w1": 1, "w64": 2, "w64x4": 3, "teams4": 4, "w1o2": 5, "fwd": 6, "pp": 7}
+FLASH_KERNELS = {"teams": 0, "w1": 1, "w64": 2, "w64x4": 3, "teams4": 4, "w1o2": 5, "fwd": 6, "pp": 7, "ks": 8}
 FLASH_SCHEDULES = {"block": 0, "balanced": 1, "pairs": 2}
 
 
@@ -98,6 +99,12 @@ def flash_configure(kernel: str | None = None, schedule: str | None = None, qb: 
     (None: the automatic choice) for every later call in this process."""
     call("nkl_flash_attn_configure", FLASH_KERNELS[kernel] if kernel else -1,
          FLASH_SCHEDULES[schedule] if schedule else -1, int(qb) if qb else -1, -1 if cpb is None else int(cpb))
+
+
+def flash_configure_polls(polls: int | None = None) -> None:
+    """Set the poll budget of the workgroup that merges a split query block
+    (None: the default 4096; 0: never wait, the last part to arrive merges)."""
+    call("nkl_flash_attn_configure_polls", -1 if polls is None else int(polls))
 
 
 def call(name: str, *args) -> int:

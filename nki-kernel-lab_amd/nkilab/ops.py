@@ -357,9 +357,18 @@ def _flash_scratch(ws_bytes: int, counter_bytes: int, dev: torch.device) -> tupl
     return ws, cnt
 
 
+# The attention entry points' stride limits (elements): between heads, and
+# between rows (32-bit byte offsets within a block of up to 256 rows).
+ATTN_MAX_HEAD_STRIDE, ATTN_MAX_ROW_STRIDE = 1 << 24, 1 << 21
+
+
+def _attn_strides_ok(t: torch.Tensor, E: int) -> bool:
+    return (t.stride(2) == 1 and t.data_ptr() % 16 == 0 and t.stride(0) % E == 0 and t.stride(1) % E == 0
+            and 0 <= t.stride(0) <= ATTN_MAX_HEAD_STRIDE and 0 <= t.stride(1) <= ATTN_MAX_ROW_STRIDE)
+
+
 def _attn_operand(t: torch.Tensor, E: int) -> torch.Tensor:
-    ok = (t.stride(2) == 1 and t.data_ptr() % 16 == 0 and t.stride(0) % E == 0 and t.stride(1) % E == 0)
-    return t if ok else t.contiguous()
+    return t if _attn_strides_ok(t, E) else t.contiguous()
 
 
 def attention_into(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
@@ -381,7 +390,7 @@ def attention_into(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.T
         scale = 1.0 / math.sqrt(d)
     E = 8 if q.element_size() == 2 else 4
     q, k, v = (_attn_operand(t, E) for t in (q, k, v))
-    o_ok = o.stride(2) == 1 and o.data_ptr() % 16 == 0 and o.stride(0) % E == 0 and o.stride(1) % E == 0
+    o_ok = _attn_strides_ok(o, E)
     out = o if o_ok else torch.empty((H, S, d), dtype=o.dtype, device=o.device)
     strides = (q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
                out.stride(0), out.stride(1))

@@ -57,3 +57,4 @@ def flash_cfg():
 
     yield _lib.flash_configure
     _lib.flash_configure()
+    _lib.flash_configure_polls()

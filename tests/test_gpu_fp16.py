@@ -117,6 +117,24 @@ def test_attention_fp16_matches_sdpa(rng, flash_cfg, qb, schedule, H, S, d):
     assert torch.equal(ops.attention(q, k, v), out)
 
 
+@pytest.mark.parametrize("schedule", ["balanced", "pairs", "block"])
+@pytest.mark.parametrize("H,Hkv,S,d", [(8, 8, 2048, 128), (3, 3, 1537, 128), (1, 1, 77, 96), (8, 2, 1000, 128),
+                                       (2, 2, 1, 128)])
+def test_attention_fp16_key_split_kernel(rng, flash_cfg, schedule, H, Hkv, S, d):
+    """The key-split kernel in fp16 (P rounded to fp16, the fp16 MFMA): within
+    1e-3 of fp32 SDPA, grouped-query heads included, and bitwise reproducible."""
+    from nkilab import ops
+
+    flash_cfg(kernel="ks", schedule=schedule)
+    q = _h(rng.standard_normal((H, S, d)))
+    k, v = (_h(rng.standard_normal((Hkv, S, d))) for _ in range(2))
+    out = ops.attention(q, k, v)
+    ref = _sdpa_cpu(_np(q), *(np.repeat(_np(t), H // Hkv, axis=0) for t in (k, v)))
+    assert rel_err(_np(out), ref) <= 1e-3, (schedule, H, Hkv, S, d)
+    np.testing.assert_allclose(_np(out)[:, 0], _np(v)[:, 0].repeat(H // Hkv, axis=0), rtol=2 ** -11, atol=0)
+    assert torch.equal(ops.attention(q, k, v), out)
+
+
 def test_attention_fp16_gqa_and_kernel_override(rng, flash_cfg):
     """Grouped-query fp16 attention; a kernel override to a bf16-only form
     falls back to the teams kernel for fp16."""
@@ -132,19 +150,98 @@ def test_attention_fp16_gqa_and_kernel_override(rng, flash_cfg):
 
 
 def test_fp16_rejected_where_unsupported(rng):
-    """fp16 has no naive attention, no naive GEMM and no softmax kernel: each
-    raises instead of running."""
+    """fp16 has no softmax kernel: it raises instead of running."""
     from nkilab import ops
 
-    q = _h(rng.standard_normal((1, 64, 64)))
-    with pytest.raises((TypeError, ValueError, RuntimeError)):
-        ops.attention(q, q, q, variant="naive")
     a = _h(rng.standard_normal((64, 64)))
-    c = torch.empty((64, 64), dtype=torch.float16, device="cuda")
-    with pytest.raises((TypeError, ValueError, RuntimeError)):
-        ops.gemm_into(a, a, c, variant="naive")
     with pytest.raises((TypeError, ValueError, RuntimeError)):
         ops.softmax(a)
+
+
+@pytest.mark.parametrize("variant", ["naive", "blocked"])
+@pytest.mark.parametrize("M,K,N", [(300, 77, 130), (64, 64, 64), (33, 1000, 5)])
+def test_gemm_fp16_any_shape(rng, variant, M, K, N):
+    """fp16 GEMMs the LDS-DMA kernel does not take (K off a multiple of 8, the
+    naive variant): the one-tile-per-wavefront kernel, within one fp16 step of
+    the exact product of the fp16 inputs plus the fp32 accumulation error."""
+    from nkilab import ops
+
+    a = _h(rng.standard_normal((M, K)))
+    b = _h(0.05 * rng.standard_normal((K, N)))
+    exact = _np(a).astype(np.float64) @ _np(b).astype(np.float64)
+    c = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    ops.gemm_into(a, b, c, variant=variant)
+    floor = K * 2.0 ** -24 * float(np.abs(_np(a)).max() * np.abs(_np(b)).max()) * 4
+    assert_within_f16_ulps(_np(c), exact, 1.0, floor)
+
+
+@pytest.mark.parametrize("H,S,d,pos0,base", [(2, 300, 128, 0, 10000.0), (4, 65, 64, 1000, 500000.0),
+                                             (1, 7, 8, 5, 10000.0)])
+def test_rope_fp16_matches_oracle(rng, H, S, d, pos0, base):
+    """fp16 RoPE: within one fp16 step of the oracle's value (float64 angles)
+    plus the fp32 angle error (relative 2e-7 of the angle, times the pair's
+    norm)."""
+    from nkilab import ops
+
+    xt = _h(rng.standard_normal((H, S, d)))
+    out = ops.rope_into(xt, torch.empty_like(xt), base, pos0)
+    assert out.dtype == torch.float16
+    ref = O.rope(_np(xt), pos0, base, O.F32)
+    angle_floor = 1e-5 + 4e-7 * (pos0 + S) * float(np.abs(_np(xt)).max())
+    assert_within_f16_ulps(_np(out), ref, 1.0, angle_floor)
+    ops.rope_into(xt, xt, base, pos0)  # in place
+    assert torch.equal(xt, out)
+
+
+@pytest.mark.parametrize("n", [4096 * 1024, 1000 * 8 + 5, 3])
+def test_swiglu_fp16_matches_oracle(rng, n):
+    """fp16 SwiGLU (vector body and scalar tail): silu and the product in fp32,
+    one rounding -- within one fp16 step of the oracle's fp32 value."""
+    from nkilab import ops
+
+    g, u = _h(3 * rng.standard_normal(n)), _h(rng.standard_normal(n))
+    y = torch.empty_like(g)
+    ops.swiglu_into(g, u, y)
+    assert_within_f16_ulps(_np(y), O.swiglu_fused(_np(g), _np(u)), 1.0, 1e-6)
+
+
+@pytest.mark.parametrize("H,Hkv,S,d", [(2, 2, 300, 64), (4, 2, 129, 128), (1, 1, 1, 32)])
+def test_naive_attention_fp16_matches_sdpa(rng, H, Hkv, S, d):
+    """The unfused attention with fp16 operands (fp32 scores, P rounded to
+    fp16): within 2e-3 of fp32 SDPA on the same fp16 inputs, and within 2e-3
+    of the fused fp16 kernel."""
+    from nkilab import ops
+
+    q = _h(rng.standard_normal((H, S, d)))
+    k = _h(rng.standard_normal((Hkv, S, d)))
+    v = _h(rng.standard_normal((Hkv, S, d)))
+    o = ops.attention(q, k, v, variant="naive")
+    assert o.dtype == torch.float16
+    kk, vv = (t.float().repeat_interleave(H // Hkv, dim=0) for t in (k, v))
+    ref = torch.nn.functional.scaled_dot_product_attention(q.float(), kk, vv, is_causal=True)
+    assert rel_err(_np(o), ref.cpu().numpy()) <= 2e-3
+    assert rel_err(_np(o), _np(ops.attention(q, k, v))) <= 2e-3
+
+
+@pytest.mark.parametrize("variant,n_kv_heads,rope_base,d_ff", [("flash_pipelined", 2, 10000.0, 1024),
+                                                                ("naive", None, None, 1024),
+                                                                ("flash_pipelined", None, 500000.0, 1000)])
+def test_decoder_float16_rope_naive_unfused(variant, n_kv_heads, rope_base, d_ff):
+    """The float16 policy on the block's other paths: rotary embeddings and
+    grouped K/V heads, the naive attention, and the unfused gate / up / SwiGLU
+    (d_ff not a multiple of the packed weight's group) -- each within 1e-3 of
+    the fp32 eager block."""
+    from nkilab.model import BlockConfig, DecoderBlock, nki_forward
+
+    torch.manual_seed(7)
+    block = DecoderBlock(BlockConfig(d_model=256, n_heads=4, d_ff=d_ff, n_kv_heads=n_kv_heads,
+                                     rope_base=rope_base)).eval()
+    x = torch.randn(200, 256)
+    with torch.no_grad():
+        ref = block(x).numpy()
+    out = nki_forward(block, x, attention_variant=variant, compute_dtype="float16")
+    assert out.dtype == torch.float32
+    assert rel_err(out.numpy(), ref) <= 1e-3
 
 
 def test_decoder_block_2048_hidden_float16_policy():

@@ -118,7 +118,8 @@ def test_noalloc_attention_rejects_shapes_beyond_its_static_scratch():
     _lib.flash_configure(kernel="teams", schedule="balanced")
     try:
         S = (1 << 24) + 64
-        rc = L.nkl_flash_attn_causal_noalloc(None, None, None, None, 1, 1, S, 128, 0, 128, 0, 128, 0, 128, 0, 128,
+        fake = ctypes.c_void_p(1 << 12)  # never dereferenced: the size check comes first
+        rc = L.nkl_flash_attn_causal_noalloc(fake, fake, fake, fake, 1, 1, S, 128, 0, 128, 0, 128, 0, 128, 0, 128,
                                              ctypes.c_float(0.1), 1, None)
         assert rc == -4, L.nkl_last_error_string()
         assert b"static scratch" in L.nkl_last_error_string()
@@ -137,11 +138,24 @@ def test_rope_and_gqa_abi_checks():
     assert L.nkl_rope(None, None, 1, 4, 8, 8, 8, 8, 8, 0, ctypes.c_float(1.0), 0, None) == -1  # base
     assert L.nkl_rope(None, None, 1, 4, 8, 8, 8, 8, 8, 0, ctypes.c_float(1e4), 9, None) == -2  # dtype
     assert L.nkl_rope(None, None, 0, 4, 8, 8, 8, 8, 8, 0, ctypes.c_float(1e4), 0, None) == 0   # empty
-    assert L.nkl_flash_attn_causal_gqa(None, None, None, None, None, 0, None, 0, 4, 3, 16, 64, 0, 64, 0, 64, 0, 64,
+    fake = ctypes.c_void_p(1 << 12)  # never dereferenced: the head-count check comes first
+    assert L.nkl_flash_attn_causal_gqa(fake, fake, fake, fake, None, 0, None, 0, 4, 3, 16, 64, 0, 64, 0, 64, 0, 64,
                                        0, 64, ctypes.c_float(0.1), 1, None) == -1
     assert b"divide" in L.nkl_last_error_string()
-    assert L.nkl_attention_naive_gqa(None, None, None, None, None, 0, 4, 0, 16, 64, 0, 64, 0, 64, 0, 64, 0, 64,
+    assert L.nkl_attention_naive_gqa(fake, fake, fake, fake, None, 0, 4, 0, 16, 64, 0, 64, 0, 64, 0, 64, 0, 64,
                                      ctypes.c_float(0.1), 1, None) == -1
+    assert b"divide" in L.nkl_last_error_string()
+    # row strides above 2^21 elements are refused (32-bit offsets within a block)
+    assert L.nkl_flash_attn_causal(fake, fake, fake, fake, 1, 16, 64, 64, (1 << 21) + 8, 64, 64, 64, 64, 64, 64,
+                                   ctypes.c_float(0.1), 1, None) == -1
+    assert b"row stride" in L.nkl_last_error_string()
+    assert L.nkl_flash_attn_causal(fake, fake, fake, fake, 1, 16, 64, (1 << 24) + 8, 64, 64, 64, 64, 64, 64, 64,
+                                   ctypes.c_float(0.1), 1, None) == -1
+    assert b"head stride" in L.nkl_last_error_string()
+    # null q/k/v/o with work to do are refused before any launch
+    assert L.nkl_flash_attn_causal(None, None, None, None, 1, 16, 64, 64, 64, 64, 64, 64, 64, 64, 64,
+                                   ctypes.c_float(0.1), 1, None) == -1
+    assert b"null" in L.nkl_last_error_string()
 
 
 def test_block_config_options_default_to_the_reference_block():
@@ -241,10 +255,11 @@ def test_fp16_dtype_code_and_policy_names():
     assert "NKL_F16 = 2" in hdr
     assert model._DTYPES["float16"] == torch.float16
     L = _lib.lib()
-    # fp16 operands: the naive GEMM variant and the naive attention refuse them (no launch)
-    assert L.nkl_gemm(None, None, None, None, 4, 4, 4, 4, 4, 4, 0, 0, 1, 0, 0, 0, 0, 2, 2, 1, None) in (-1, -2)
+    # fp16 operands: the naive GEMM variant and the naive attention take them,
+    # and here refuse the null pointers instead (no launch)
+    assert L.nkl_gemm(None, None, None, None, 4, 4, 4, 4, 4, 4, 0, 0, 1, 0, 0, 0, 0, 2, 2, 1, None) == -1
     assert L.nkl_attention_naive(None, None, None, None, None, 1 << 20, 1, 16, 64, 64, 64, 64, 64, 64, 64, 64, 64,
-                                 ctypes.c_float(0.1), 2, None) == -2
+                                 ctypes.c_float(0.1), 2, None) == -1
     assert L.nkl_flash_attn_causal_workspace_bytes(8, 2048, 128, 2) > 0
 
 
