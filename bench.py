@@ -13,11 +13,14 @@ meets 1e-3 against the fp32 block, with the all-bf16 and split-operand ones
 beside it).
 
 Timing: every kernel is launched from a captured HIP graph (so host launch
-overhead does not leave the GPU idle between launches), replayed K times
-between two HIP events recorded on the stream the kernels run on; the result
-is the average duration per launch.  Each graph cycles through enough
-distinct input/output buffers (> 256 MB) that no launch finds its data in the
-MI355X's 256 MB last-level cache: the row kernels are measured against HBM.
+overhead does not leave the GPU idle between launches), replayed at least 50
+times with a HIP event recorded on the graph's stream after every replay; the
+result is the median over the replays of one replay's duration over its
+launches.  Each graph cycles through enough distinct input/output buffers
+(at least twice the MI355X's 256 MB last-level cache) that no launch finds
+its data there: every kernel is measured against HBM.  The decoder block is
+the exception: one input and its ~100 MB of weights serve every launch, and
+its entry says so ("llc").
 
 CPU baseline: the oracle's NumPy restatement of the reference's flash
 algorithm (the "NKI-algorithm CPU path") timed on this host, plus PyTorch CPU
@@ -46,13 +49,14 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def time_launches(launches, reps: int, warmup: int) -> float:
-    """Seconds per launch: capture `launches` (zero-arg callables, one kernel
-    each) into a HIP graph, replay it `warmup` times, then `reps` times between
-    two events on the current stream.  The eager warm-up runs on the stream
-    the capture uses, so that per-stream scratch (the attention's partial
-    states and counters) exists before capture and no allocation or fill is
-    captured into the timed graph."""
+MIN_REPLAYS = 50
+
+
+def capture(launches):
+    """A HIP graph of `launches` (zero-arg callables, one call each).  An eager
+    pass runs first on the stream the capture uses, so that per-stream scratch
+    (the attention's partial states and counters) exists before capture and
+    no allocation or fill is captured."""
     import torch
 
     side = torch.cuda.Stream()
@@ -66,16 +70,29 @@ def time_launches(launches, reps: int, warmup: int) -> float:
     with torch.cuda.graph(graph, stream=side):
         for f in launches:
             f()
+    torch.cuda.synchronize()
+    return graph
+
+
+def time_launches(launches, reps: int, warmup: int) -> float:
+    """Seconds per launch: the median, over max(reps, 50) replays of the graph
+    of `launches`, of one replay's duration (between two HIP events recorded
+    on the stream the graph runs on) over its number of launches."""
+    import torch
+
+    graph = capture(launches)
     for _ in range(warmup):
         graph.replay()
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(reps):
+    n = max(reps, MIN_REPLAYS)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    ev[0].record()
+    for i in range(n):
         graph.replay()
-    end.record()
+        ev[i + 1].record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) * 1e-3 / (reps * len(launches))
+    per = sorted(ev[i].elapsed_time(ev[i + 1]) * 1e-3 / len(launches) for i in range(n))
+    return per[n // 2] if n % 2 else 0.5 * (per[n // 2 - 1] + per[n // 2])
 
 
 def n_sets(bytes_per_set: int) -> int:
@@ -105,7 +122,7 @@ def bench_attention(H, S, d, reps, warmup, seed=0, sets=None):
 
     q, k, v = (t.cuda() for t in workloads.attention_inputs(H, S, d, seed=seed))
     per_set = 4 * H * S * d * 2
-    sets = sets or min(n_sets(per_set), 16)
+    sets = sets or n_sets(per_set)
     bufs = [(q, k, v, torch.empty_like(q))] + [
         (q.clone(), k.clone(), v.clone(), torch.empty_like(q)) for _ in range(sets - 1)]
     launches = [lambda b=b: ops.attention_into(*b) for b in bufs]
@@ -128,7 +145,7 @@ def bench_attention_beside_sdpa(reps, warmup):
     for H, S in ((8, 2048), (1, 4096), (8, 8192), (32, 16384)):
         q, k, v = (t.cuda() for t in workloads.attention_inputs(H, S, 128))
         big = S > 8192
-        sets = 2 if big else min(n_sets(4 * H * S * 128 * 2), 16)
+        sets = n_sets(4 * H * S * 128 * 2)
         bufs = [(q, k, v, torch.empty_like(q))] + [
             (q.clone(), k.clone(), v.clone(), torch.empty_like(q)) for _ in range(sets - 1)]
         r = max(3, reps // 10) if big else reps
@@ -160,7 +177,7 @@ def bench_attention_sweep(reps, warmup):
     for H, S in ((1, 256), (1, 1024), (1, 2048), (8, 512), (8, 1024), (2, 2048), (4, 2048), (8, 2048), (16, 2048),
                  (8, 4096)):
         q, k, v = (t.cuda() for t in workloads.attention_inputs(H, S, 128))
-        sets = min(n_sets(4 * H * S * 128 * 2), 16)
+        sets = n_sets(4 * H * S * 128 * 2)
         bufs = [(q.clone(), k.clone(), v.clone(), torch.empty_like(q)) for _ in range(sets)]
         sec = time_launches([lambda b=b: ops.attention_into(*b) for b in bufs], reps, warmup)
         flops = workloads.causal_flops(H, S, 128)
@@ -263,7 +280,7 @@ def bench_matmul(reps, warmup):
 
     a, b = (t.cuda() for t in workloads.matmul_inputs())
     sets = n_sets(3 * 1024 * 1024 * 2)
-    bufs = [(a.clone(), b.clone(), torch.empty_like(a)) for _ in range(min(sets, 64))]
+    bufs = [(a.clone(), b.clone(), torch.empty_like(a)) for _ in range(sets)]
     sec = time_launches([lambda t=t: ops.gemm_into(*t) for t in bufs], reps, warmup)
     flops = 2 * 1024 ** 3
     return {"M": 1024, "N": 1024, "K": 1024, "us": sec * 1e6, "tflops": flops / sec / 1e12,
@@ -289,7 +306,7 @@ def bench_gemm_shapes(reps, warmup):
     for M, N, K, kind in GEMM_SHAPES:
         per_set = 2 * (M * K + N * K + 2 * M * N)
         sets = []
-        for _ in range(min(n_sets(per_set), 8)):
+        for _ in range(n_sets(per_set)):
             a = torch.randn(M, K, device="cuda", generator=gen).to(torch.bfloat16)
             b = torch.randn(*((K, N) if kind == "nn" else (N, K)), device="cuda", generator=gen).to(torch.bfloat16)
             sets.append((a, b, torch.empty(M, N, device="cuda", dtype=torch.bfloat16),
@@ -340,6 +357,7 @@ def bench_decoder(reps, warmup, counters=None):
                      "rel_err_vs_fp32_block": err, "launches": launches}
     rep = out["fp16"]
     return {"us": rep["us"], "tflops": rep["tflops"], "rel_err_vs_fp32_block": rep["rel_err_vs_fp32_block"],
+            "llc": "warm: one input and the block's weights (~100 MB) serve every launch",
             "compute": "fp16 activations and weights (fp32 accumulation, fp32 residual stream), P rounded to fp16",
             "roofline": roofline("mfma", rep["tflops"], "TFLOP/s", (counters or {}).get("decoder")),
             "flops_per_step": flops, "fp16_activations": out["fp16"], "bf16_activations": out["bf16"],
@@ -486,7 +504,7 @@ def cpu_rows_baseline(ncores: int) -> dict:
 # MFMAs issued, SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512.  Written by
 #     python bench.py --collect-counters OUT
 # which runs one rocprofv3 pass per workload and counter set over
-# `bench.py --pmc-pass WORKLOAD` (eager launches on cold buffers).
+# `bench.py --pmc-pass WORKLOAD` (graph-replayed launches, as in the timing).
 
 COUNTERS_FILE = os.path.join(ROOT, "profiles", "counters.json")
 COPY_BYTES = 256 << 20
@@ -507,43 +525,45 @@ PMC_REPS = 8
 # Calls of the workload in one counter pass where not PMC_REPS.  Counters are
 # reported per call: a call can be several dispatches (the decoder forward;
 # the gate/up GEMM split over two column ranges).
-PMC_CALLS = {"attention_32x16384": 2, "decoder": 2}
+PMC_CALLS = {"attention_32x16384": 2, "attention_1x4096": 16, "decoder": 2}
 
 
 def pmc_pass(workload: str) -> None:
-    """Eager launches for one counter pass: the calibration copy, then the
-    workload PMC_REPS times on rotating buffer sets (cold last-level cache)."""
+    """Launches for one counter pass, as the timing runs them: the workload's
+    calls (PMC_REPS of them, or PMC_CALLS, on rotating buffer sets) captured
+    in a HIP graph after one eager pass, then the calibration copy, then one
+    replay of the graph.  parse_counters() counts only the dispatches after
+    the last calibration copy: the replayed ones."""
     import torch
 
     from nkilab import ops, workloads
 
-    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
-    dst = torch.empty_like(src)
-    for _ in range(3):
-        torch.neg(src, out=dst)  # one streaming read and write of COPY_BYTES each
-    torch.cuda.synchronize()
-    del src, dst
+    calls = []
+    keep = []  # the buffers the graph's calls use
     if workload.startswith("attention"):
         H, S = {"attention": (8, 2048), "attention_1x4096": (1, 4096), "attention_32x16384": (32, 16384)}[workload]
         q, k, v = (t.cuda() for t in workloads.attention_inputs(H, S, 128))
-        n = 2 if S > 8192 else PMC_REPS
-        sets = [(q.clone(), k.clone(), v.clone(), torch.empty_like(q)) for _ in range(2 if S > 8192 else 16)]
-        for i in range(n):
-            ops.attention_into(*sets[i % len(sets)])
+        n = PMC_CALLS.get(workload, PMC_REPS)
+        sets = [(q.clone(), k.clone(), v.clone(), torch.empty_like(q)) for _ in range(n)]
+        keep.append(sets)
+        calls = [lambda b=b: ops.attention_into(*b) for b in sets]
     elif workload == "matmul":
         a, b = (t.cuda() for t in workloads.matmul_inputs())
-        sets = [(a.clone(), b.clone(), torch.empty_like(a)) for _ in range(64)]
-        for i in range(PMC_REPS):
-            ops.gemm_into(*sets[i])
+        sets = [(a.clone(), b.clone(), torch.empty_like(a)) for _ in range(PMC_REPS)]
+        keep.append(sets)
+        calls = [lambda t=t: ops.gemm_into(*t) for t in sets]
     elif workload in ("softmax", "rmsnorm", "swiglu"):
         x, w, gate, up = (t.cuda() for t in workloads.rows_inputs(4096, 2048))
-        for i in range(PMC_REPS):
-            if workload == "softmax":
-                ops.softmax_into(x.clone(), torch.empty_like(x))
-            elif workload == "rmsnorm":
-                ops.rmsnorm_into(x.clone(), w, torch.empty_like(x), 1e-6)
-            else:
-                ops.swiglu_into(gate.clone(), up.clone(), torch.empty_like(gate))
+        if workload == "softmax":
+            sets = [(x.clone(), torch.empty_like(x)) for _ in range(PMC_REPS)]
+            calls = [lambda t=t: ops.softmax_into(*t) for t in sets]
+        elif workload == "rmsnorm":
+            sets = [(x.clone(), torch.empty_like(x)) for _ in range(PMC_REPS)]
+            calls = [lambda t=t: ops.rmsnorm_into(t[0], w, t[1], 1e-6) for t in sets]
+        else:
+            sets = [(gate.clone(), up.clone(), torch.empty_like(gate)) for _ in range(PMC_REPS)]
+            calls = [lambda t=t: ops.swiglu_into(*t) for t in sets]
+        keep.append(sets)
     elif workload in DECODER_GEMMS or workload in ("gemm_4096", "hipblaslt_4096"):
         M, N, K = DECODER_GEMMS.get(workload, (4096, 4096, 4096))
         g = torch.Generator().manual_seed(0)
@@ -556,24 +576,34 @@ def pmc_pass(workload: str) -> None:
                 sets.append((a, w, torch.empty(M, N // 2, dtype=torch.bfloat16, device="cuda")))
             else:
                 sets.append((a, w, torch.empty(M, N, dtype=torch.bfloat16, device="cuda")))
+        keep.append(sets)
         for i in range(PMC_REPS):
+            t = sets[i % 4]
             if workload == "gemm_gate_up":
-                ops.gemm_swiglu_into(*sets[i % 4])
+                calls.append(lambda t=t: ops.gemm_swiglu_into(*t))
             elif workload == "hipblaslt_4096":  # torch.mm: the hipBLASLt kernel on the same operands
-                torch.mm(sets[i % 4][0], sets[i % 4][1].t(), out=sets[i % 4][2])
+                calls.append(lambda t=t: torch.mm(t[0], t[1].t(), out=t[2]))
             else:
-                ops.linear_into(*sets[i % 4])
+                calls.append(lambda t=t: ops.linear_into(*t))
     elif workload == "decoder":
         from nkilab.model import nki_forward
 
         block, x = workloads.decoder_inputs()
         block, xg = block.cuda(), x.cuda()
-        for _ in range(2):
-            nki_forward(block, xg, compute_dtype="float16")
+        keep.append((block, xg))
+        calls = [lambda: nki_forward(block, xg, compute_dtype="float16")] * PMC_CALLS["decoder"]
     else:
         raise SystemExit(f"unknown counter workload {workload!r}; one of {sorted(PMC_WORKLOADS)}")
+    graph = capture(calls)
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)  # one streaming read and write of COPY_BYTES each
     torch.cuda.synchronize()
-    log(f"pmc pass {workload} done")
+    del src, dst
+    graph.replay()
+    torch.cuda.synchronize()
+    log(f"pmc pass {workload} done ({len(calls)} graph-replayed calls)")
 
 
 def collect_counters(out_dir: str, only: list[str] | None = None) -> dict:
@@ -636,10 +666,14 @@ def parse_counters(out_dir: str, only: list[str] | None = None) -> dict:
         for tag in ("fetch", "write", "mfma"):
             per = {}  # counter -> (sum over the workload's dispatches, dispatches)
             calib = {}
-            for name, ctr, val, did in _rows(csv_of(wl, tag)):
+            rows = list(_rows(csv_of(wl, tag)))
+            last_calib = max(did for name, _, _, did in rows if "neg_kernel" in name)
+            for name, ctr, val, did in rows:
                 if "neg_kernel" in name:
                     calib[ctr] = calib.get(ctr, 0.0) + val / 3.0
                     continue
+                if did < last_calib:
+                    continue  # the eager pass before the graph's capture
                 if pat and pat not in name:
                     continue
                 if not pat and ("elementwise" in name or "Fill" in name or "copy" in name.lower()):

@@ -17,8 +17,14 @@
  *     and the causal attention; see each entry point).
  *   - `stream` is a hipStream_t passed as void* (0 = the null stream).  Every
  *     call only enqueues work and returns; it is asynchronous with respect to
- *     the host and re-entrant (no global state besides the per-thread error
- *     string).
+ *     the host.  State kept across calls: the per-thread error string; the
+ *     process-wide attention configuration (nkl_flash_attn_configure and
+ *     nkl_flash_attn_configure_polls, and the NKL_FLASH_* / NKL_GEMM_TILE
+ *     environment read once); a per-device cache of the CU count; and the
+ *     per-device static scratch of nkl_flash_attn_causal_noalloc.  Calls are
+ *     safe from several threads at once, except that a configuration change
+ *     must not overlap attention calls that size or launch under it, and
+ *     noalloc calls that may overlap on one device race on its scratch.
  *   - Return value: NKL_OK (0) on success, a negative NKL_E* code otherwise;
  *     nkl_last_error_string() describes the last failure on this thread.
  */

@@ -11,13 +11,20 @@ on this GPU, so the reference's site/index.html renders measured data:
     graph, warm inputs); they keep the reference's field names
     (``modeled_latency_us``, ``modeled_tflops``) and each summary says
     ``"latency_source": "measured"``;
-  * ``hbm_bytes`` is the compulsory traffic of the call (inputs read once,
-    outputs written once);
+  * ``hbm_bytes`` is the HBM traffic rocprofv3 measured for the same kernel
+    and shape (FETCH_SIZE + WRITE_SIZE, profiles/counters.json, written by
+    ``bench.py --collect-counters``) where there is such a measurement, else
+    the compulsory traffic of the call (inputs read once, outputs written
+    once); ``hbm_bytes_source`` says which, and ``compulsory_hbm_bytes`` is
+    always the latter;
+  * ``engine_busy_pct`` holds the measured MFMA busy share of the SIMDs
+    (``{"mfma": ...}``, SQ_VALU_MFMA_BUSY_CYCLES over the dispatch's SIMD
+    cycles, same file) where measured;
   * trace events are one per kernel call, from HIP events around calls
     queued back to back behind a short spin kernel (lane ``"HIP stream"``),
     or one per dispatch from a rocprofv3 kernel-trace CSV (lane ``"queue N"``);
-  * fields with no measured counterpart on a GPU (instruction counts, engine
-    busy shares, on-chip footprints) are null.
+  * fields with no measured counterpart on a GPU (instruction counts, other
+    engines' busy shares, on-chip footprints) are null or empty.
 
     python -m nkilab.results --out results.json [--quick] [--rocprof-csv kernel_trace.csv]
 """
@@ -60,10 +67,33 @@ LADDER = [
 
 # ------------------------------------------------------------- summaries --
 
+COUNTERS_FILE = os.path.join(os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))),
+                             "profiles", "counters.json")
+
+
+def load_counters(path: str = COUNTERS_FILE) -> dict:
+    """rocprofv3 counter results per workload (profiles/counters.json), or {}."""
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return {}
+
+
 def summary(kernel: str, latency_us: float, hbm_bytes: int, flops: int, dtype: str = "bfloat16",
-            compulsory: int | None = None, extra: dict | None = None) -> dict:
+            compulsory: int | None = None, extra: dict | None = None, counters: dict | None = None) -> dict:
     """One kernel's entry, field for field the reference's Profile.summary
-    (profiler.py:210-235) plus run() additions (run_bench.py:44-58)."""
+    (profiler.py:210-235) plus run() additions (run_bench.py:44-58).
+    `counters` is the kernel's entry of profiles/counters.json when this call
+    is the measured workload (same kernel and shape): its HBM bytes replace
+    the computed ones and its MFMA busy share fills engine_busy_pct."""
+    source = "computed (compulsory traffic)"
+    busy = {}
+    if counters and counters.get("bytes"):
+        hbm_bytes = counters["bytes"]
+        source = "measured: rocprofv3 FETCH_SIZE + WRITE_SIZE per launch (profiles/counters.json)"
+    if counters and counters.get("mfma_busy") is not None:
+        busy = {"mfma": round(100.0 * counters["mfma_busy"], 2)}
     peak = HARDWARE["peak_flops"].get(dtype, HARDWARE["peak_flops"]["float32"])
     bw = HARDWARE["hbm_bytes_per_s"]
     t_compute, t_memory = flops / peak, hbm_bytes / bw
@@ -75,6 +105,7 @@ def summary(kernel: str, latency_us: float, hbm_bytes: int, flops: int, dtype: s
         "per_engine": {},
         "dma_bytes": {"hbm_to_sbuf": None, "sbuf_to_hbm": None, "other": None},
         "hbm_bytes": int(hbm_bytes),
+        "hbm_bytes_source": source,
         "flops": int(flops),
         "modeled_latency_us": latency_us,
         "latency_source": "measured",
@@ -84,7 +115,7 @@ def summary(kernel: str, latency_us: float, hbm_bytes: int, flops: int, dtype: s
         "arithmetic_intensity": flops / hbm_bytes if hbm_bytes else None,
         "modeled_tflops": flops / lat_s / 1e12 if lat_s > 0 else 0.0,
         "pct_of_roofline": bound_s / lat_s * 100 if lat_s > 0 else 0.0,
-        "engine_busy_pct": {},
+        "engine_busy_pct": busy,
         "peak_sbuf_bytes_per_partition": None,
         "peak_psum_bytes_per_partition": None,
         "sbuf_capacity_ok": None,
@@ -250,6 +281,7 @@ def bench_matmul(quick: bool) -> dict:
     from . import ops
 
     n = 512 if quick else 1024
+    ctr = load_counters()
     rng = _rng()
     a, b = (_gpu(rng.standard_normal((n, n)), torch.bfloat16) for _ in range(2))
     ref = a.double() @ b.double()
@@ -260,7 +292,8 @@ def bench_matmul(quick: bool) -> dict:
         us = time_us(lambda: ops.gemm_into(a, b, c, variant=nm))
         err = float((c.double() - ref).abs().max() / ref.abs().max())
         label = "matmul naive" if nm == "naive" else "matmul blocked (MFMA, LDS-DMA)"
-        variants.append(summary(label, us, comp, 2 * n**3, compulsory=comp, extra={"rel_err_vs_numpy": err}))
+        variants.append(summary(label, us, comp, 2 * n**3, compulsory=comp, extra={"rel_err_vs_numpy": err},
+                                counters=ctr.get("matmul") if nm == "blocked" and n == 1024 else None))
     sweep = []
     for m in ([512, 1024] if quick else [512, 1024, 2048]):
         x = torch.zeros((m, m), dtype=torch.bfloat16, device="cuda")
@@ -280,6 +313,8 @@ def bench_norm(quick: bool) -> dict:
     from . import ops
 
     R, D = (1024, 1024) if quick else (4096, 2048)
+    full = not quick  # the profiled shape
+    ctr = load_counters()
     rng = _rng()
     x = _gpu(rng.standard_normal((R, D)) * 3, torch.bfloat16)
     y = torch.empty_like(x)
@@ -290,13 +325,16 @@ def bench_norm(quick: bool) -> dict:
         # three passes: read x twice (max, exp), write and re-read fp32 e
         nbytes = 2 * R * D * 2 if fused else R * D * (2 + 2 + 4 + 4 + 2)
         variants.append(summary(nm, us, nbytes, 0, compulsory=2 * R * D * 2,
+                                counters=ctr.get("softmax") if fused and full else None,
                                 extra={"max_abs_err_vs_torch": float((y.float() - ref).abs().max())}))
     w = _gpu(rng.uniform(0.5, 1.5, D), torch.bfloat16)
     us = time_us(lambda: ops.rmsnorm_into(x, w, y, 1e-6))
-    variants.append(summary("rmsnorm fused", us, 2 * R * D * 2 + D * 2, 0, compulsory=2 * R * D * 2 + D * 2))
+    variants.append(summary("rmsnorm fused", us, 2 * R * D * 2 + D * 2, 0, compulsory=2 * R * D * 2 + D * 2,
+                            counters=ctr.get("rmsnorm") if full else None))
     u = _gpu(rng.standard_normal((R, D)), torch.bfloat16)
     us = time_us(lambda: ops.swiglu_into(x, u, y))
-    variants.append(summary("swiglu fused", us, 3 * R * D * 2, 0, compulsory=3 * R * D * 2))
+    variants.append(summary("swiglu fused", us, 3 * R * D * 2, 0, compulsory=3 * R * D * 2,
+                            counters=ctr.get("swiglu") if full else None))
     return {"shape": [R, D], "variants": variants}
 
 
@@ -307,6 +345,7 @@ def bench_attention(quick: bool) -> dict:
     from . import ops
 
     H, S, d = (2, 512, 64) if quick else (8, 2048, 128)
+    ctr = load_counters()
     rng = _rng()
     q, k, v = (_gpu(rng.standard_normal((H, S, d)), torch.bfloat16) for _ in range(3))
     o = torch.empty_like(q)
@@ -321,7 +360,8 @@ def bench_attention(quick: bool) -> dict:
         err = float((o.float() - ref).abs().max() / ref.abs().max())
         ladder.append(summary(label, us, comp, exact, compulsory=comp,
                               extra={"useful_causal_flops": useful, "rel_err_vs_torch": err,
-                                     "variant": var}))
+                                     "variant": var},
+                              counters=ctr.get("attention") if var != "naive" and not quick else None))
     scaling = []
     for s_len in ([256, 512] if quick else [512, 1024, 2048, 4096]):
         qz = torch.zeros((1, s_len, d), dtype=torch.bfloat16, device="cuda")

@@ -27,6 +27,27 @@ def test_summary_has_every_reference_field():
     assert m["roofline_regime"] == "memory" and m["roofline_bound_us"] == pytest.approx(33_554_432 / 8e12 * 1e6)
 
 
+def test_summary_takes_measured_counters():
+    """With the kernel's counter entry, hbm_bytes is the measured traffic (the
+    compulsory bytes stay beside it) and engine_busy_pct the MFMA busy share;
+    without one, the computed bytes and an empty busy dict."""
+    from nkilab import results as R
+
+    s = R.summary("softmax fused", 6.0, 33_554_432, 0, compulsory=33_554_432,
+                  counters={"bytes": 33_615_213, "mfma_busy": 0.0})
+    assert s["hbm_bytes"] == 33_615_213 and s["compulsory_hbm_bytes"] == 33_554_432
+    assert s["hbm_bytes_source"].startswith("measured")
+    assert s["engine_busy_pct"] == {"mfma": 0.0}
+    a = R.summary("flash", 24.0, 16_777_216, 8_598_323_200, counters={"bytes": 39_525_525, "mfma_busy": 0.1048})
+    assert a["engine_busy_pct"] == {"mfma": 10.48}
+    assert a["roofline_bound_us"] == pytest.approx(max(8_598_323_200 / 2.5166e15, 39_525_525 / 8e12) * 1e6)
+    c = R.summary("swiglu fused", 9.0, 50_331_648, 0)
+    assert c["hbm_bytes"] == 50_331_648 and c["hbm_bytes_source"].startswith("computed")
+    assert c["engine_busy_pct"] == {}
+    ctr = R.load_counters()
+    assert ctr == {} or all(k in ctr for k in ("attention", "softmax", "matmul"))
+
+
 def test_short_kernel_names():
     from nkilab.results import short_kernel_name as k
 
