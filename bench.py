@@ -273,6 +273,80 @@ def bench_copy_curve(reps, warmup):
             "kernel": "nkl_stream_copy (2 x 16-byte loads per lane, non-temporal stores)"}
 
 
+def bench_row_curve(reps, warmup):
+    """The row kernels (bf16, 2048 columns) and the streaming copy from 1 to
+    256 MiB of traffic, each size its own graph in the usual harness: time per
+    launch against bytes moved, and a least-squares line per kernel that
+    splits a launch into a fixed cost and a steady bandwidth."""
+    import torch
+
+    from nkilab import _lib, ops
+    from nkilab._tensors import stream_handle
+
+    D = 2048
+    out = {}
+
+    def fit(points):
+        xs = [p["bytes"] for p in points]
+        ys = [p["us"] for p in points]
+        n = len(xs)
+        mx, my = sum(xs) / n, sum(ys) / n
+        slope = sum((x - mx) * (y - my) for x, y in zip(xs, ys)) / sum((x - mx) ** 2 for x in xs)
+        return {"fixed_us": round(my - slope * mx, 3), "steady_GB/s": round(1e-3 / slope, 1)}
+
+    for name in ("copy", "softmax", "rmsnorm", "swiglu"):
+        points = []
+        for R in (128, 256, 512, 1024, 2048, 4096, 8192, 16384, 32768):
+            w = torch.ones(D, dtype=torch.bfloat16, device="cuda")
+            if name == "swiglu":
+                nbytes = 3 * R * D * 2
+                sets = [(torch.randn(R, D, device="cuda").to(torch.bfloat16),
+                         torch.randn(R, D, device="cuda").to(torch.bfloat16),
+                         torch.empty(R, D, dtype=torch.bfloat16, device="cuda")) for _ in range(n_sets(nbytes))]
+                calls = [lambda t=t: ops.swiglu_into(*t) for t in sets]
+            else:
+                nbytes = 2 * R * D * 2 + (D * 2 if name == "rmsnorm" else 0)
+                sets = [(torch.randn(R, D, device="cuda").to(torch.bfloat16),
+                         torch.empty(R, D, dtype=torch.bfloat16, device="cuda")) for _ in range(n_sets(nbytes))]
+                if name == "copy":
+                    calls = [lambda t=t: _lib.call("nkl_stream_copy", t[0].data_ptr(), t[1].data_ptr(), R * D * 2,
+                                                   stream_handle()) for t in sets]
+                elif name == "softmax":
+                    calls = [lambda t=t: ops.softmax_into(*t) for t in sets]
+                else:
+                    calls = [lambda t=t: ops.rmsnorm_into(t[0], w, t[1], 1e-6) for t in sets]
+            us = time_launches(calls, reps, warmup) * 1e6
+            points.append({"rows": R, "bytes": nbytes, "us": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1),
+                           "frac": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4), "buffer_sets": len(sets)})
+            log(f"  {name} {R}x{D}: {us:.2f} us {nbytes / us / 1e3:.0f} GB/s")
+            del sets, calls
+        out[name] = {"points": points, "fit": fit(points)}
+    return out
+
+
+def summarize_trace(csv_path: str) -> str:
+    """A markdown table of a rocprofv3 kernel-trace CSV: dispatches grouped by
+    kernel and grid size, with their count and median / average / minimum
+    duration in microseconds."""
+    import csv
+    import statistics
+
+    groups = {}
+    with open(csv_path) as f:
+        for row in csv.DictReader(f):
+            name = row.get("Kernel_Name") or row.get("Kernel-Name") or ""
+            grid = int(row.get("Grid_Size") or row.get("Grid_Size_X") or 0)
+            wg = int(row.get("Workgroup_Size") or row.get("Workgroup_Size_X") or 0)
+            dur = (int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1000.0
+            groups.setdefault((name, grid, wg), []).append(dur)
+    lines = ["| kernel | workgroups x threads | dispatches | median us | avg us | min us |", "|---|---|---|---|---|---|"]
+    for (name, grid, wg), ds in sorted(groups.items(), key=lambda kv: (kv[0][0], kv[0][1])):
+        short = name.split("(")[0]
+        lines.append(f"| `{short}` | {grid // max(wg, 1)} x {wg} | {len(ds)} | {statistics.median(ds):.3f} | "
+                     f"{sum(ds) / len(ds):.3f} | {min(ds):.3f} |")
+    return "\n".join(lines)
+
+
 def bench_matmul(reps, warmup):
     import torch
 
@@ -723,6 +797,10 @@ def main() -> int:
     ap.add_argument("--sdpa", action="store_true", help="only attention beside torch SDPA, one JSON line")
     ap.add_argument("--attention-sweep", action="store_true",
                     help="only attention time per launch over sizes up to the headline, one JSON line")
+    ap.add_argument("--row-curve", action="store_true",
+                    help="only the row kernels and the copy over sizes from 1 to 256 MiB, one JSON line")
+    ap.add_argument("--summarize-trace", metavar="CSV",
+                    help="print a rocprofv3 kernel-trace CSV as a table of durations per kernel and grid")
     ap.add_argument("--report", default=None, help="write the full result dict as JSON here")
     ap.add_argument("--pmc-pass", metavar="WORKLOAD", help="eager launches of one workload for a rocprofv3 --pmc run")
     ap.add_argument("--collect-counters", metavar="OUT",
@@ -732,6 +810,9 @@ def main() -> int:
     ap.add_argument("--workloads", default=None,
                     help="with --collect-counters: only these comma-separated workloads (the others keep their entries)")
     args = ap.parse_args()
+    if args.summarize_trace:
+        print(summarize_trace(args.summarize_trace))
+        return 0
     if args.parse_counters:
         out = parse_counters(os.path.abspath(args.parse_counters))
         with open(COUNTERS_FILE, "w") as f:
@@ -771,6 +852,9 @@ def main() -> int:
         return 0
     if args.attention_sweep:
         print(json.dumps({"attention_sweep": bench_attention_sweep(args.steps, args.warmup)}), flush=True)
+        return 0
+    if args.row_curve:
+        print(json.dumps({"row_curve": bench_row_curve(args.steps, args.warmup)}), flush=True)
         return 0
 
     ctr = load_counters()
