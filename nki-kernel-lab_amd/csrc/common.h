@@ -331,6 +331,30 @@ __device__ __forceinline__ __attribute__((address_space(3))) void* lds_ptr(unsig
 // hands x on as the wait's output, so that no use of x precedes the wait.
 __device__ __forceinline__ void lds_wait_tie(bf16x8& x) { asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x)); }
 
+// Brings the kernel's argument block into the scalar cache at the kernel's
+// start: one scalar load per 64-byte line, issued together, then one wait.
+// The compiler fetches a large argument block lazily, in many dependent
+// batches each waited for at once (and mostly spilled to VGPR lanes under
+// register pressure); every batch that touches a new line of the block waits
+// a scalar-cache miss.  Warm, those batches hit.  BYTES: the size of the
+// kernel's arguments.  (Loads only; the values are discarded.)
+template <int BYTES>
+__device__ __forceinline__ void prefetch_kernargs() {
+  static_assert(BYTES > 0 && BYTES <= 8 * 64, "argument block of 1 to 8 lines");
+  constexpr int LINES = (BYTES + 63) / 64;
+  const auto kp = __builtin_amdgcn_kernarg_segment_ptr();
+  int a[8];
+#pragma unroll
+  for (int l = 0; l < LINES; ++l) asm volatile("s_load_dword %0, %1, %2" : "=s"(a[l]) : "s"(kp), "i"(64 * l));
+  // The loaded values are inputs of the wait, so that each load has a
+  // register of its own.
+  constexpr int L1 = LINES > 1 ? 1 : 0, L2 = LINES > 2 ? 2 : 0, L3 = LINES > 3 ? 3 : 0, L4 = LINES > 4 ? 4 : 0,
+                L5 = LINES > 5 ? 5 : 0, L6 = LINES > 6 ? 6 : 0, L7 = LINES > 7 ? 7 : 0;
+  asm volatile("s_waitcnt lgkmcnt(0)" ::"s"(a[0]), "s"(a[L1]), "s"(a[L2]), "s"(a[L3]), "s"(a[L4]), "s"(a[L5]),
+               "s"(a[L6]), "s"(a[L7])
+               : "memory");
+}
+
 __device__ __forceinline__ bf16x8 load_frag(const bf16* p) {
   return *reinterpret_cast<const bf16x8*>(p);
 }

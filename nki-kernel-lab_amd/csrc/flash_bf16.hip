@@ -96,7 +96,7 @@ __device__ __forceinline__ bf16x8 read_vt_frag(const bf16* row_a, const bf16* ro
 
 }  // namespace
 
-template <int D, int WPT, int NT, bool H = false>
+template <int D, int WPT, int NT, bool H = false, bool F = false>
 // Two wavefronts per SIMD (at most 256 registers each): a 4-wavefront
 // workgroup then shares its CU with a second one.  H: fp16 operands, P and O
 // (the 16-bit values move as raw bits; only the MFMA and the roundings of P
@@ -113,6 +113,7 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
   __shared__ __align__(16) bf16 smem[L::SMEM];
   __shared__ int arrival;
 
+  prefetch_kernargs<sizeof(AttnArgs) + sizeof(Work)>();
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int team = wid / WPT, wq = wid % WPT;
@@ -142,11 +143,11 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
   const int vfrag_off = L::K_ELEMS + (4 * h32 + (i16 >> 2)) * L::LDV + 16 * g2 + 4 * (i16 & 3);
 
   long u0, u1;
-  const int vidx = wg_range(w, p.H, u0, u1);  // this workgroup's range index and units [u0, u1)
+  const int vidx = wg_range_x<F>(w, p.H, u0, u1);  // this workgroup's range index and units [u0, u1)
 
   // The segment of the range that ends with unit u (fsched::decode_seg: a
   // range is walked from its last segment to its first).
-  auto decode = [&](long u) __attribute__((always_inline)) { return decode_seg(u, u0, w); };
+  auto decode = [&](long u) __attribute__((always_inline)) { return decode_seg_x<F>(u, u0, w); };
   auto load_q = [&](const Seg& sg, bf16x8 (&q)[NQF]) __attribute__((always_inline)) {
     const bf16* Q = static_cast<const bf16*>(p.q) + (long)sg.hh * p.q_sh;
     const int qrow = QB * sg.b + 32 * wq + l32;
@@ -517,8 +518,8 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
     // ---- finish the query block, or hand a partial state to the last arriver
     int nparts = 1, vf = vidx;
     if (w.sched == kBalanced) {
-      vf = range_of(bstart, w);
-      nparts = range_of(bstart + nt_b - 1, w) - vf + 1;
+      vf = range_of_x<F>(bstart, w);
+      nparts = range_of_x<F>(bstart + nt_b - 1, w) - vf + 1;
     }
     if (nparts == 1) {
       store_out();
@@ -533,7 +534,7 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
       auto poff = [&](int v, int s, int k) __attribute__((always_inline)) {
         return 4 * (((v * 2 + s) * L::PART) + wq * L::SLOT + k * 256 + 4 * lane);
       };
-      const int slot = range_start(vidx, w) >= bstart ? 0 : 1;
+      const int slot = range_start_x<F>(vidx, w) >= bstart ? 0 : 1;
       auto pstore = [&](int k, float4 x) __attribute__((always_inline)) {
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), prsrc, poff(vidx, slot, k), 0,
                                                kDeviceCoherent);
@@ -578,7 +579,7 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
 #pragma unroll 1
         for (int v2 = vl; v2 >= vf; --v2) {
           if (v2 == vidx && vidx == vl) continue;
-          const int slot2 = range_start(v2, w) >= bstart ? 0 : 1;
+          const int slot2 = range_start_x<F>(v2, w) >= bstart ? 0 : 1;
           fold_state([&](int k) __attribute__((always_inline)) {
             return __builtin_bit_cast(float4,
                                       __builtin_amdgcn_raw_buffer_load_b128(prsrc, poff(v2, slot2, k), 0, kDeviceCoherent));
@@ -624,10 +625,11 @@ constexpr int W1_STAGEB = 2 * W1_TILEB;     // K tile then V tile
 
 }  // namespace
 
-template <int QH, int NW, int OCC = 1>
+template <int QH, int NW, int OCC = 1, bool F = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
 void flash_bf16_w1_kernel(AttnArgs p, Work w) {
   static_assert((QH == 1 || QH == 2) && (NW == 2 || NW == 4), "32 or 64 queries per wavefront, 2 or 4 wavefronts");
+  prefetch_kernargs<sizeof(AttnArgs) + sizeof(Work)>();
   constexpr int D = 128, NQF = D / 16, NDB = D / 32, QW = 32 * QH, QB = QW * NW;
   // Partial state of one 32-query half: NCO float4 chunks of O and one of
   // (m, l) per lane.
@@ -687,10 +689,10 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
   }
 
   long u0, u1;
-  const int vidx = wg_range(w, p.H, u0, u1);  // this workgroup's range index and units [u0, u1)
+  const int vidx = wg_range_x<F>(w, p.H, u0, u1);  // this workgroup's range index and units [u0, u1)
 
   // The segment of the range that ends with unit u (fsched::decode_seg).
-  auto decode = [&](long u) __attribute__((always_inline)) { return decode_seg(u, u0, w); };
+  auto decode = [&](long u) __attribute__((always_inline)) { return decode_seg_x<F>(u, u0, w); };
   bf16x8 qf[QH][NQF];
   auto load_q = [&](const Seg& sg) __attribute__((always_inline)) {
     const bf16* Q = static_cast<const bf16*>(p.q) + (long)sg.hh * p.q_sh;
@@ -1025,8 +1027,8 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
 
     int nparts = 1, vf = vidx;
     if (w.sched == kBalanced) {
-      vf = range_of(bstart, w);
-      nparts = range_of(bstart + nt_b - 1, w) - vf + 1;
+      vf = range_of_x<F>(bstart, w);
+      nparts = range_of_x<F>(bstart + nt_b - 1, w) - vf + 1;
     }
     if (nparts == 1) {
       store_out();
@@ -1037,7 +1039,7 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
       auto poff = [&](int v, int s2, int hq, int k) __attribute__((always_inline)) {
         return 4 * (((v * 2 + s2) * PART) + wq * SLOT + hq * HS + k * 256 + 4 * lane);
       };
-      const int slot = range_start(vidx, w) >= bstart ? 0 : 1;
+      const int slot = range_start_x<F>(vidx, w) >= bstart ? 0 : 1;
       const int vl = vf + nparts - 1;
       if (vidx == vl) await_parts(&w.count[hh * w.nqb + b], nparts, w.polls, arrival);
       const bool stored = vidx != vl || arrival != nparts - 1;
@@ -1079,7 +1081,7 @@ void flash_bf16_w1_kernel(AttnArgs p, Work w) {
 #pragma unroll 1
         for (int v2 = vl; v2 >= vf; --v2) {
           if (v2 == vidx && vidx == vl) continue;
-          const int slot2 = range_start(v2, w) >= bstart ? 0 : 1;
+          const int slot2 = range_start_x<F>(v2, w) >= bstart ? 0 : 1;
 #pragma unroll
           for (int hq = 0; hq < QH; ++hq) {
             // (m, l) first, then O one d-block (4 float4 per lane) at a time.
@@ -1325,17 +1327,30 @@ size_t part_floats_for(int d, const Config& cfg) {
   return d <= 32 ? part_floats<32>(cfg.qb) : d <= 64 ? part_floats<64>(cfg.qb) : part_floats<128>(cfg.qb);
 }
 
+// Kernels are instantiated twice over their schedule arithmetic: 32-bit only
+// when the plan fits (Work::fast, every realistic shape), else 64-bit.
 template <int D, int WPT, int NT>
 void launch(const AttnArgs& a, const Work& w, hipStream_t st) {
-  if (a.f16)
-    flash_bf16_kernel<D, WPT, NT, true><<<dim3((unsigned)w.grid), dim3(64 * WPT * NT), 0, st>>>(a, w);
-  else
-    flash_bf16_kernel<D, WPT, NT, false><<<dim3((unsigned)w.grid), dim3(64 * WPT * NT), 0, st>>>(a, w);
+  const dim3 grid((unsigned)w.grid), block(64 * WPT * NT);
+  if (a.f16) {
+    if (w.fast)
+      flash_bf16_kernel<D, WPT, NT, true, true><<<grid, block, 0, st>>>(a, w);
+    else
+      flash_bf16_kernel<D, WPT, NT, true, false><<<grid, block, 0, st>>>(a, w);
+  } else {
+    if (w.fast)
+      flash_bf16_kernel<D, WPT, NT, false, true><<<grid, block, 0, st>>>(a, w);
+    else
+      flash_bf16_kernel<D, WPT, NT, false, false><<<grid, block, 0, st>>>(a, w);
+  }
 }
 
 template <int QH, int NW, int OCC = 1>
 void launch_w(const AttnArgs& a, const Work& w, hipStream_t st) {
-  flash_bf16_w1_kernel<QH, NW, OCC><<<dim3((unsigned)w.grid), dim3(64 * NW), 0, st>>>(a, w);
+  if (w.fast)
+    flash_bf16_w1_kernel<QH, NW, OCC, true><<<dim3((unsigned)w.grid), dim3(64 * NW), 0, st>>>(a, w);
+  else
+    flash_bf16_w1_kernel<QH, NW, OCC, false><<<dim3((unsigned)w.grid), dim3(64 * NW), 0, st>>>(a, w);
 }
 
 template <int D>

@@ -87,7 +87,7 @@ using I = std::integral_constant<int, N>;
 
 }  // namespace
 
-template <bool PP>
+template <bool PP, bool F = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void flash_fwd_kernel(AttnArgs p, Work w) {
   using namespace fwd;
@@ -95,6 +95,7 @@ void flash_fwd_kernel(AttnArgs p, Work w) {
   __shared__ __align__(16) unsigned char lds[LDS_BYTES];
   __shared__ int arrival;
 
+  prefetch_kernargs<sizeof(AttnArgs) + sizeof(Work)>();
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wq = wid & 3, kh = wid >> 2;
@@ -137,7 +138,7 @@ void flash_fwd_kernel(AttnArgs p, Work w) {
   }
 
   long u0, u1;
-  const int vidx = wg_range(w, p.H, u0, u1);
+  const int vidx = wg_range_x<F>(w, p.H, u0, u1);
 
   bf16x8 qf[8];
   auto load_q = [&](const Seg& sg) __attribute__((always_inline)) {
@@ -185,7 +186,7 @@ void flash_fwd_kernel(AttnArgs p, Work w) {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
   };
 
-  Seg cur = decode_seg(u1 - 1, u0, w);
+  Seg cur = decode_seg_x<F>(u1 - 1, u0, w);
   Src src = seg_src(cur);
   if constexpr (PP) {
     // The first segment's Q block is copied once for the workgroup into the
@@ -629,7 +630,7 @@ void flash_fwd_kernel(AttnArgs p, Work w) {
     const long next_u = bstart + t0 - 1;  // the last unit of the previous segment
     const bool more = next_u >= u0;
     Seg nxt = cur;
-    if (more) nxt = decode_seg(next_u, u0, w);
+    if (more) nxt = decode_seg_x<F>(next_u, u0, w);
     bar();  // every wavefront is done with the stages
     const Src nsrc = seg_src(nxt);
     if (more) {
@@ -727,8 +728,8 @@ void flash_fwd_kernel(AttnArgs p, Work w) {
     // ---- finish the query block, or hand a partial state to the last arriver
     int nparts = 1, vf = vidx;
     if (w.sched == kBalanced) {
-      vf = range_of(bstart, w);
-      nparts = range_of(bstart + cur.nt - 1, w) - vf + 1;
+      vf = range_of_x<F>(bstart, w);
+      nparts = range_of_x<F>(bstart + cur.nt - 1, w) - vf + 1;
     }
     if (nparts == 1) {
       store_out(own, l_tot);
@@ -740,7 +741,7 @@ void flash_fwd_kernel(AttnArgs p, Work w) {
       const __amdgpu_buffer_rsrc_t prsrc =
           __builtin_amdgcn_make_buffer_rsrc(w.part, (short)0, w.part_bytes, kBufferFlags);
       auto pbase = [&](int v) __attribute__((always_inline)) {
-        const int s = range_start(v, w) >= bstart ? 0 : 1;
+        const int s = range_start_x<F>(v, w) >= bstart ? 0 : 1;
         return ((v * 2 + s) * 8 + wid) * (PCH * 1024) + lane * 16;
       };
       // The holder of the block's last range merges: it waits for the other
@@ -825,10 +826,20 @@ void flash_fwd_kernel(AttnArgs p, Work w) {
 }
 
 void launch_flash_fwd(const AttnArgs& a, const Work& w, bool pingpong, hipStream_t st) {
-  if (pingpong)
-    flash_fwd_kernel<true><<<dim3((unsigned)w.grid), dim3(512), 0, st>>>(a, w);
-  else
-    flash_fwd_kernel<false><<<dim3((unsigned)w.grid), dim3(512), 0, st>>>(a, w);
+  // Instantiated over the schedule arithmetic too: 32-bit only when the plan
+  // fits (Work::fast).
+  const dim3 grid((unsigned)w.grid), block(512);
+  if (pingpong) {
+    if (w.fast)
+      flash_fwd_kernel<true, true><<<grid, block, 0, st>>>(a, w);
+    else
+      flash_fwd_kernel<true, false><<<grid, block, 0, st>>>(a, w);
+  } else {
+    if (w.fast)
+      flash_fwd_kernel<false, true><<<grid, block, 0, st>>>(a, w);
+    else
+      flash_fwd_kernel<false, false><<<grid, block, 0, st>>>(a, w);
+  }
 }
 
 size_t flash_fwd_part_bytes() { return fwd::PART_BYTES; }

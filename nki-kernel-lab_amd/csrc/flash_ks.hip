@@ -70,6 +70,10 @@ constexpr int KS_XML = 0;
 constexpr int KS_XO = 2048;
 constexpr int KS_XSLOT = 8 * 64 * 16;
 static_assert(KS_XO + 12 * KS_XSLOT <= KS_QOFF, "exchange area overlaps Q");
+// Parts of a split block a wavefront stages per round trip of the merge:
+// ten 1 KB chunks each, in its 32 KB of K/V buffers.
+constexpr int KS_MB = 3;
+static_assert(KS_MB * 10 * 1024 <= KS_WAVEB, "merge staging fits a wavefront's buffers");
 // A part's state in the workspace (floats): per d-block 8 float4 chunks per
 // lane (the wavefront finishing it stores them), then (m, l, 0, 0) per lane
 // and half.
@@ -232,6 +236,7 @@ void flash_ks_kernel(AttnArgs p, Work w) {
   // Alone on its SIMD: declaring an AGPR use makes the compiler keep the O
   // accumulators in AGPRs.
   asm volatile("" ::: "a255");
+  prefetch_kernargs<sizeof(AttnArgs) + sizeof(Work)>();
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wq = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -382,9 +387,13 @@ void flash_ks_kernel(AttnArgs p, Work w) {
     };
     float m_run[2], l_run[2];
     floatx16 oacc[2][NDB];
+    // K(0), K(1) and V(0) go out with Q, so that their latencies overlap:
+    // one wait for Q and K(0), the others land during S(0).
     copy_k(0, 0);
-    __builtin_amdgcn_s_waitcnt(0);  // Q and K(0) have landed
-    __builtin_amdgcn_s_barrier();   // ... for every wavefront (Q)
+    copy_k(1, 1);
+    copy_v(0, 0);
+    wait_vm<16>();                 // Q and K(0) have landed (K(1), V(0) in flight)
+    __builtin_amdgcn_s_barrier();  // ... for every wavefront (Q)
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     {
       bf16x8 k0f[NQF];
@@ -401,28 +410,24 @@ void flash_ks_kernel(AttnArgs p, Work w) {
         lds_wait_tie_acc(qf[1][f]);
         lds_wait_tie(k0f[f]);
       }
-      // S(0), with the copies of K(1) and V(0) one per MFMA; O starts at zero
-      // (MFMAs of zeros, so that O is made in the registers it stays in).
-      const __amdgpu_buffer_rsrc_t rk1 = tile_rsrc(p.k, p.k_sh, 1);
-      const __amdgpu_buffer_rsrc_t rv0 = tile_rsrc(p.v, p.v_sh, 0);
+      // S(0), with the copies of K(2) into K buffer 0 (its fragments are in
+      // registers) one per odd MFMA; O starts at zero (MFMAs of zeros, so that
+      // O is made in the registers it stays in).
+      const __amdgpu_buffer_rsrc_t rk2 = tile_rsrc(p.k, p.k_sh, 2);
 #pragma unroll
       for (int k = 0; k < 2 * NQF; ++k) {
         if (k < 2)
           qk_first<H>(s0[k & 1], k0f[k >> 1], qf[k & 1][k >> 1]);
         else
           qk_acc<H>(s0[k & 1], k0f[k >> 1], qf[k & 1][k >> 1]);
-        if (k < 8)
-          copy1(rk1, wb + KS_TILEB, k);
-        else
-          copy1(rv0, wb + KS_VOFF, k - 8);
+        if (k & 1) copy1(rk2, wb, k >> 1);
       }
       o_zero<H>(oacc);
-      wait_vm<8>();  // K(1) has landed
+      wait_vm<16>();  // K(1) has landed (V(0), K(2) in flight)
 #pragma unroll
       for (int f = 0; f < NQF; ++f) kf[f] = ds_b128_f<KS_TILEB>(kbase, f);
 #pragma unroll
       for (int f = 0; f < NQF; ++f) lds_wait_tie(kf[f]);
-      copy_k(2, 0);  // K buffer 0 is free again
       wait_vm<8>();  // V(0) has landed
       read_v(std::integral_constant<int, 0>{}, va);
       tie_v(va);
@@ -600,6 +605,11 @@ void flash_ks_kernel(AttnArgs p, Work w) {
       if (i + 1 >= ntw) break;
       step(kOdd, kMasked, i + 1, s1, s0, k2, kf, v2, va);
     }
+    // A split block's arrival count, read now so that its latency overlaps the
+    // exchange below (only thread 0's value is used).
+    int arrived = 0;
+    if (w.sched == kBalanced && tid == 0) arrived = __hip_atomic_load(&w.count[hh * w.nqb + b], __ATOMIC_RELAXED,
+                                                                      __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_s_waitcnt(0);  // every copy (the tiles past the segment too) has landed
     o_settle(oacc);
     __syncthreads();
@@ -715,8 +725,9 @@ void flash_ks_kernel(AttnArgs p, Work w) {
         return 4 * ((v * 2 + s2) * KS_PARTF + 4 * KS_PDB + (hq * 64 + lane) * 4);
       };
       const int slot = range_start_t<int>(vidx, w) >= bstart ? 0 : 1;
-      // Every other part has already arrived: merge without storing this one.
-      if (tid == 0) flag = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nparts - 1;
+      // Every other part has already arrived (the count was read before the
+      // exchange): merge without storing this one.
+      if (tid == 0) flag = arrived == nparts - 1;
       __syncthreads();
       if (!flag) {
 #pragma unroll
@@ -739,60 +750,82 @@ void flash_ks_kernel(AttnArgs p, Work w) {
         __syncthreads();
       }
       if (flag) {
-        // Fold every part in range order, this one from registers.
+        // Fold every part into a running state in range order (this one from
+        // registers): the largest max so far, the sum and O rescaled to it.
+        // The other parts' chunks for this lane -- (m, l) of both halves and
+        // d-block wq of O, ten 1 KB chunks per wavefront and part -- are
+        // copied by the buffer unit into this wavefront's K/V buffers (free
+        // after the exchange), KS_MB parts per memory round trip, and read
+        // back from there: no registers held for them.
         const int vl = vf + nparts - 1;
-        float Mt[2] = {-INFINITY, -INFINITY};
-#pragma unroll 1
-        for (int v2 = vf; v2 <= vl; ++v2) {
-          const int s2 = range_start_t<int>(v2, w) >= bstart ? 0 : 1;
-#pragma unroll
-          for (int hq = 0; hq < 2; ++hq) {
-            const float m2 = v2 == vidx ? M[hq]
-                                        : __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                                         prs, mlbyte(v2, s2, hq), 0, kDeviceCoherent))
-                                              .x;
-            Mt[hq] = fmaxf(Mt[hq], m2);
-          }
-        }
-        float Lt[2] = {0.f, 0.f};
+        float Mt[2] = {-INFINITY, -INFINITY}, Lt[2] = {0.f, 0.f};
         floatx16 acc[2];
 #pragma unroll
         for (int hq = 0; hq < 2; ++hq)
 #pragma unroll
           for (int e = 0; e < 16; ++e) acc[hq][e] = 0.f;
-#pragma unroll 1
-        for (int v2 = vf; v2 <= vl; ++v2) {
-          const int s2 = range_start_t<int>(v2, w) >= bstart ? 0 : 1;
-          if (v2 == vidx) {
+        // Folds a part with maxima m2, sums l2 and O chunks getx(hq, k4).
+        auto fold = [&](const float (&m2)[2], const float (&l2)[2], auto getx) __attribute__((always_inline)) {
 #pragma unroll
-            for (int hq = 0; hq < 2; ++hq) {
-              const float a2 = M[hq] == -INFINITY ? 0.f : fast_exp2(M[hq] - Mt[hq]);
-              Lt[hq] = fmaf(L[hq], a2, Lt[hq]);
+          for (int hq = 0; hq < 2; ++hq) {
+            const float Mn = fmaxf(Mt[hq], m2[hq]);
+            const float a1 = Mt[hq] == -INFINITY ? 0.f : fast_exp2(Mt[hq] - Mn);
+            const float a2 = m2[hq] == -INFINITY ? 0.f : fast_exp2(m2[hq] - Mn);
+            Mt[hq] = Mn;
+            Lt[hq] = fmaf(l2[hq], a2, Lt[hq] * a1);
 #pragma unroll
-              for (int e = 0; e < 16; ++e) acc[hq][e] = fmaf(fin[hq][e], a2, acc[hq][e]);
+            for (int k4 = 0; k4 < 4; ++k4) {
+              const float4 x = getx(hq, k4);
+              acc[hq][4 * k4] = fmaf(x.x, a2, acc[hq][4 * k4] * a1);
+              acc[hq][4 * k4 + 1] = fmaf(x.y, a2, acc[hq][4 * k4 + 1] * a1);
+              acc[hq][4 * k4 + 2] = fmaf(x.z, a2, acc[hq][4 * k4 + 2] * a1);
+              acc[hq][4 * k4 + 3] = fmaf(x.w, a2, acc[hq][4 * k4 + 3] * a1);
             }
-          } else {
+          }
+        };
+        // Staging of part i of a batch: chunk j (j < 8: O chunk 4 hq + k4;
+        // 8, 9: (m, l) of half j - 8) at stg + (10 i + j) KB, lane l's 16
+        // bytes at + 16 l.
+        const unsigned stg = wb;
+        const float4* stgp = reinterpret_cast<const float4*>(lds + wq * KS_WAVEB) + lane;
+#pragma unroll 1
+        for (int v0 = vf; v0 <= vl; v0 += KS_MB) {
 #pragma unroll
-            for (int hq = 0; hq < 2; ++hq) {
-              const float4 ml =
-                  __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(prs, mlbyte(v2, s2, hq), 0,
-                                                                                   kDeviceCoherent));
-              float4 x[4];
+          for (int i = 0; i < KS_MB; ++i) {
+            const int v2 = v0 + i;
+            if (v2 <= vl && v2 != vidx) {
+              const int s2 = range_start_t<int>(v2, w) >= bstart ? 0 : 1;
 #pragma unroll
-              for (int k4 = 0; k4 < 4; ++k4)
-                x[k4] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                       prs, obyte(v2, s2, wq, 4 * hq + k4), 0, kDeviceCoherent));
-              const float a2 = ml.x == -INFINITY ? 0.f : fast_exp2(ml.x - Mt[hq]);
-              Lt[hq] = fmaf(ml.y, a2, Lt[hq]);
-#pragma unroll
-              for (int k4 = 0; k4 < 4; ++k4) {
-                acc[hq][4 * k4] = fmaf(x[k4].x, a2, acc[hq][4 * k4]);
-                acc[hq][4 * k4 + 1] = fmaf(x[k4].y, a2, acc[hq][4 * k4 + 1]);
-                acc[hq][4 * k4 + 2] = fmaf(x[k4].z, a2, acc[hq][4 * k4 + 2]);
-                acc[hq][4 * k4 + 3] = fmaf(x[k4].w, a2, acc[hq][4 * k4 + 3]);
+              for (int j = 0; j < 10; ++j) {
+                // (The offset and the LDS address go through locals: written
+                // inline in the builtin's arguments they made the host pass
+                // drop this kernel's launch stub without a diagnostic.)
+                const int off = j < 8 ? obyte(v2, s2, wq, j) : mlbyte(v2, s2, j - 8);
+                const unsigned dst = stg + (10 * i + j) * 1024;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(prs, lds_ptr(dst), 16, off, 0, 0, kDeviceCoherent);
               }
             }
           }
+          __builtin_amdgcn_s_waitcnt(0);  // the batch has landed in LDS
+          __atomic_signal_fence(__ATOMIC_SEQ_CST);
+#pragma unroll
+          for (int i = 0; i < KS_MB; ++i) {
+            const int v2 = v0 + i;
+            if (v2 > vl) continue;
+            if (v2 == vidx) {
+              fold(M, L, [&](int hq, int k4) __attribute__((always_inline)) {
+                return make_float4(fin[hq][4 * k4], fin[hq][4 * k4 + 1], fin[hq][4 * k4 + 2], fin[hq][4 * k4 + 3]);
+              });
+            } else {
+              const float4 ml0 = stgp[(10 * i + 8) * 64], ml1 = stgp[(10 * i + 9) * 64];
+              const float m2[2] = {ml0.x, ml1.x}, l2[2] = {ml0.y, ml1.y};
+              fold(m2, l2, [&](int hq, int k4) __attribute__((always_inline)) {
+                return stgp[(10 * i + 4 * hq + k4) * 64];
+              });
+            }
+          }
+          __atomic_signal_fence(__ATOMIC_SEQ_CST);
+          __builtin_amdgcn_s_waitcnt(0xC07F);  // the batch is read before the next one lands (lgkmcnt(0))
         }
 #pragma unroll
         for (int hq = 0; hq < 2; ++hq) {

@@ -230,6 +230,38 @@ __device__ __forceinline__ int wg_range_fast(const Work& w, int H, int& u0, int&
   return vidx;
 }
 
+// The schedule arithmetic with the unit type chosen at compile time: F true
+// (the plan's Work::fast holds: every value fits in 32 bits) takes the 32-bit
+// paths only, so that a kernel instantiated for it carries no 64-bit
+// division code (which the compiler would otherwise set up at the kernel's
+// start and keep in registers throughout).
+template <bool F>
+__device__ __forceinline__ int wg_range_x(const Work& w, int H, long& u0, long& u1) {
+  if constexpr (F) {
+    int a, b;
+    const int v = wg_range_fast(w, H, a, b);
+    u0 = a;
+    u1 = b;
+    return v;
+  } else {
+    return wg_range(w, H, u0, u1);
+  }
+}
+template <bool F>
+__device__ __forceinline__ int range_of_x(long u, const Work& w) {
+  if constexpr (F)
+    return range_of_t<int>((int)u, w);
+  else
+    return range_of(u, w);
+}
+template <bool F>
+__device__ __forceinline__ long range_start_x(long v, const Work& w) {
+  if constexpr (F)
+    return range_start_t<int>((int)v, w);
+  else
+    return range_start(v, w);
+}
+
 // A segment: head hh, query block b, tiles [t0, t1) of the block's nt tiles,
 // whose first unit is bstart.
 struct Seg {
@@ -278,6 +310,13 @@ __host__ __device__ __forceinline__ Seg decode_seg_t(I u, I u0, const Work& w) {
 }
 __host__ __device__ __forceinline__ Seg decode_seg(long u, long u0, const Work& w) {
   return w.fast ? decode_seg_t<int>((int)u, (int)u0, w) : decode_seg_t<long>(u, u0, w);
+}
+template <bool F>
+__device__ __forceinline__ Seg decode_seg_x(long u, long u0, const Work& w) {
+  if constexpr (F)
+    return decode_seg_t<int>((int)u, (int)u0, w);
+  else
+    return decode_seg_t<long>(u, u0, w);
 }
 
 // The workgroup holding a split block's last range merges it.  It walks that

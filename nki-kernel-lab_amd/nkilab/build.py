@@ -61,8 +61,25 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
         out = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
         if out.returncode != 0:
             raise RuntimeError(f"link failed:\n{out.stdout}")
+        missing = undefined_own_symbols(tmp_lib)
+        if missing:
+            os.remove(tmp_lib)
+            raise RuntimeError("the library leaves its own symbols undefined (a kernel whose launch stub the host "
+                               "pass did not emit?):\n" + "\n".join(missing))
         os.replace(tmp_lib, LIB_PATH)
     return LIB_PATH
+
+
+def undefined_own_symbols(lib: str) -> list[str]:
+    """Symbols of the library's own namespace (nkl::) that `lib` references
+    but does not define: a shared library links with them, and fails only
+    when loaded.  Empty when nm is not available."""
+    nm = shutil.which("nm")
+    if not nm:
+        return []
+    out = subprocess.run([nm, "-D", "--undefined-only", lib], stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                         text=True)
+    return [ln.split()[-1] for ln in out.stdout.splitlines() if ln.split() and ln.split()[-1].startswith("_ZN3nkl")]
 
 
 def _wait(item, verbose):
