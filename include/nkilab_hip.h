@@ -270,6 +270,22 @@ int nkl_flash_attn_configure(int kernel, int schedule, int qb, int cpb);
 int nkl_flash_attn_configure_polls(int polls);
 
 /*
+ * Test hook, host only (no GPU work): checks the work split the 16-bit
+ * attention kernels would walk for an H x S x d call (dtype NKL_BF16 or
+ * NKL_F16) under the configuration in force.  Balanced ranges tile the
+ * units in order and none is empty; walking each range from its last
+ * segment to its first, as the kernels do, covers it exactly; every split
+ * block's parts are the ranges that hold its units and its last range is
+ * the one that merges; no range puts two parts in one of its two partial-
+ * state slots; the pairs and block schedules take every block whole, once.
+ * Returns NKL_OK, NKL_EDTYPE for other dtypes, or NKL_EINVAL naming the
+ * first violated invariant (or a shape outside d <= 128).  info
+ * (NULL or 4 longs): workgroups, units, split blocks, most parts of a block.
+ * No counterpart in the reference (its kernels have no work split).
+ */
+int nkl_flash_attn_plan_check(int H, int S, int d, int dtype, long* info);
+
+/*
  * Unfused causal attention: scores (fp32, [H, S, S]) and probabilities
  * ([H, S, S], dtype) are materialised in `workspace`, then O = P V.
  * Replaces nkilab/kernels/attention.py:35 (attention_naive), selected by

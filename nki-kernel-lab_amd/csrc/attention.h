@@ -47,5 +47,7 @@ size_t flash_ks_part_bytes();
 int flash_bf16_configure(int kern, int sched, int qb, int cpb);
 // Process-wide poll budget of the workgroup that merges a split block (-1: 4096).
 int flash_bf16_configure_polls(int polls);
+// Host-side check of the launch plan's work split (flash_bf16.hip).
+int flash_bf16_plan_check(int H, int S, int d, bool f16, long* info);
 
 }  // namespace nkl

@@ -488,6 +488,12 @@ extern "C" int nkl_flash_attn_configure(int kernel, int schedule, int qb, int cp
 
 extern "C" int nkl_flash_attn_configure_polls(int polls) { return flash_bf16_configure_polls(polls); }
 
+extern "C" int nkl_flash_attn_plan_check(int H, int S, int d, int dtype, long* info) {
+  if (dtype != NKL_BF16 && dtype != NKL_F16)
+    return set_error(NKL_EDTYPE, "nkl_flash_attn_plan_check: the 16-bit kernels only (dtype %d)", dtype);
+  return flash_bf16_plan_check(H, S, d, dtype == NKL_F16, info);
+}
+
 extern "C" size_t nkl_attention_naive_workspace_bytes(int H, int S, int dtype) {
   if (H <= 0 || S <= 0) return 0;
   const size_t n = (size_t)H * S * S;

@@ -41,6 +41,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <vector>
+
 #include "attention.h"
 #include "flash_sched.h"
 
@@ -1382,6 +1384,121 @@ size_t flash_bf16_counter_bytes(int H, int S) {
   if (H <= 0 || S <= 0) return 0;
   if (choose(H, S, 32, false).sched != kBalanced && choose(H, S, 128, false).sched != kBalanced) return 0;
   return (size_t)H * ((S + 63) / 64) * 4;
+}
+
+// Host-side check of the launch plan for an H x S x d call under the
+// configuration in force: the work split the kernels walk, invariant by
+// invariant.  Balanced ranges tile the units in order, none empty; walking a
+// range from its last segment to its first (as the kernels do) covers its
+// units exactly; range_of agrees with the range that holds a unit; a split
+// block's parts are the ranges that hold its units, its last range the one
+// that merges; no range puts two parts in one of its two partial-state
+// slots.  Pairs and blocks: every block taken by exactly one workgroup.
+// info (optional, 4 longs): grid, units, split blocks, largest part count.
+int flash_bf16_plan_check(int H, int S, int d, bool f16, long* info) {
+  if (H < 1 || S < 1 || d < 1 || d > 128)
+    return set_error(NKL_EINVAL, "plan check: shape H=%d S=%d d=%d outside the kernels' range", H, S, d);
+  const Config cfg = choose(H, S, d, f16);
+  const Work w = plan(H, S, cfg);
+  auto fail = [&](const char* what, long x, long y) {
+    return set_error(NKL_EINVAL, "plan check H=%d S=%d d=%d (kernel %d, schedule %d, qb %d, cpb %d, grid %d): %s "
+                     "(%ld, %ld)", H, S, d, cfg.kern, cfg.sched, cfg.qb, w.cpb, w.grid, what, x, y);
+  };
+  if (w.grid < 1) return fail("empty grid", w.grid, 0);
+  std::vector<int> owner(w.units, -1);
+  long split = 0, max_parts = 1;
+  if (cfg.sched == kBalanced) {
+    if (fsched::range_start(0, w) != 0) return fail("range 0 does not start at unit 0", fsched::range_start(0, w), 0);
+    if (fsched::range_start(w.grid, w) != w.units)
+      return fail("the last range does not end at the last unit", fsched::range_start(w.grid, w), w.units);
+    std::vector<int> slot_used(2L * w.grid, 0);
+    for (int v = 0; v < w.grid; ++v) {
+      const long u0 = fsched::range_start(v, w), u1 = fsched::range_start(v + 1, w);
+      if (u1 <= u0) return fail("empty range", v, u0);
+      // The 32-bit instances (magic divisors) must agree with the 64-bit ones.
+      if (w.fast && fsched::range_start_t<long>(v, w) != u0)
+        return fail("32- and 64-bit range starts differ", u0, fsched::range_start_t<long>(v, w));
+      long u = u1 - 1, covered = 0;
+      for (int guard = 0; guard <= w.units; ++guard) {
+        const fsched::Seg sg = fsched::decode_seg(u, u0, w);
+        if (w.fast) {
+          const fsched::Seg sl = fsched::decode_seg_t<long>(u, u0, w);
+          if (sl.hh != sg.hh || sl.b != sg.b || sl.t0 != sg.t0 || sl.t1 != sg.t1 || sl.bstart != sg.bstart)
+            return fail("32- and 64-bit segment decodes differ", u, sl.bstart);
+        }
+        if (sg.t0 < 0 || sg.t1 > sg.nt || sg.t0 >= sg.t1) return fail("segment tiles out of order", sg.t0, sg.t1);
+        if (sg.bstart + sg.t1 - 1 != u) return fail("segment does not end at its unit", sg.bstart + sg.t1 - 1, u);
+        if (sg.bstart + sg.t0 != (u0 > sg.bstart ? u0 : sg.bstart))
+          return fail("segment does not start at its range or block", sg.bstart + sg.t0, u0);
+        for (long x = sg.bstart + sg.t0; x < sg.bstart + sg.t1; ++x) {
+          if (owner[x] != -1) return fail("unit covered twice", x, v);
+          owner[x] = v;
+          ++covered;
+        }
+        const int vf = fsched::range_of(sg.bstart, w), vl = fsched::range_of(sg.bstart + sg.nt - 1, w);
+        if (vf > v || vl < v) return fail("range_of disagrees with the segment's range", vf, vl);
+        if (vl > vf) {
+          const int slot = fsched::range_start(v, w) >= sg.bstart ? 0 : 1;
+          if (slot_used[2 * v + slot]++) return fail("two parts in one slot", v, slot);
+          if (v == vf && sg.t0 != 0) return fail("the block's first part does not start it", v, sg.t0);
+          if (v == vl && sg.t1 != sg.nt) return fail("the merging range does not end the block", v, sg.t1);
+          if (v == vl) {
+            ++split;
+            max_parts = max_parts > vl - vf + 1 ? max_parts : vl - vf + 1;
+          }
+        }
+        const long next_u = sg.bstart + sg.t0 - 1;
+        if (next_u < u0) break;
+        u = next_u;
+      }
+      if (covered != u1 - u0) return fail("a range's segments do not cover it", covered, u1 - u0);
+    }
+    for (long x = 0; x < w.units; ++x) {
+      if (fsched::range_of(x, w) != owner[x]) return fail("range_of disagrees with the owner", x, owner[x]);
+      if (w.fast && fsched::range_of_t<long>(x, w) != owner[x])
+        return fail("32- and 64-bit range_of differ", x, fsched::range_of_t<long>(x, w));
+    }
+  } else {
+    // One workgroup per pair of blocks (pairs) or per block (fsched::wg_range
+    // for workgroup g), walked like a balanced range: whole blocks only.
+    for (int g = 0; g < w.grid; ++g) {
+      const int hh = g % H;
+      long u0, u1;
+      if (cfg.sched == kPairs) {
+        const int k = g / H;
+        u0 = (long)hh * w.units_head + fsched::pair_before(k, w);
+        u1 = 2 * k + 2 <= w.nqb ? (long)hh * w.units_head + fsched::pair_before(k + 1, w) : (long)(hh + 1) * w.units_head;
+      } else {
+        const int b = w.nqb - 1 - g / H;
+        u0 = (long)hh * w.units_head + fsched::plain_before(b, w);
+        u1 = u0 + fsched::block_tiles(b, w);
+      }
+      if (u1 <= u0) return fail("empty workgroup", g, u0);
+      long u = u1 - 1;
+      for (int guard = 0; guard <= w.units; ++guard) {
+        const fsched::Seg sg = fsched::decode_seg(u, u0, w);
+        if (sg.t0 != 0 || sg.t1 != sg.nt) return fail("a block split without the balanced schedule", g, sg.t0);
+        if (sg.bstart + sg.t1 - 1 != u) return fail("segment does not end at its unit", sg.bstart + sg.t1 - 1, u);
+        for (long x = sg.bstart; x < sg.bstart + sg.nt; ++x) {
+          if (x < 0 || x >= w.units) return fail("unit out of range", x, g);
+          if (owner[x] != -1) return fail("unit covered twice", x, g);
+          owner[x] = g;
+        }
+        const long next_u = sg.bstart - 1;
+        if (next_u < u0) break;
+        u = next_u;
+      }
+    }
+  }
+  for (long x = 0; x < w.units; ++x)
+    if (owner[x] < 0) return fail("unit not covered", x, 0);
+  if (info) {
+    info[0] = w.grid;
+    info[1] = w.units;
+    info[2] = split;
+    info[3] = max_parts;
+  }
+  return NKL_OK;
 }
 
 int flash_bf16_launch(const AttnArgs& a, void* workspace, size_t workspace_bytes, int* counters,

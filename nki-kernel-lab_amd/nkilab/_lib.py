@@ -55,6 +55,7 @@ SIGNATURES = {
                           _c_int, _vp]),
     "nkl_flash_attn_configure": (_c_int, [_c_int, _c_int, _c_int, _c_int]),
     "nkl_flash_attn_configure_polls": (_c_int, [_c_int]),
+    "nkl_flash_attn_plan_check": (_c_int, [_c_int, _c_int, _c_int, _c_int, _vp]),
     "nkl_attention_naive_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int]),
     "nkl_attention_naive": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_size, _c_int, _c_int, _c_int, _c_long, _c_long,
                                      _c_long, _c_long, _c_long, _c_long, _c_long, _c_long, _c_float, _c_int, _vp]),
@@ -105,6 +106,16 @@ def flash_configure_polls(polls: int | None = None) -> None:
     """Set the poll budget of the workgroup that merges a split query block
     (None: the default 4096; 0: never wait, the last part to arrive merges)."""
     call("nkl_flash_attn_configure_polls", -1 if polls is None else int(polls))
+
+
+def flash_plan_check(H: int, S: int, d: int, f16: bool = False) -> tuple[int, int, int, int]:
+    """Check on the host the work split the 16-bit attention kernels would
+    walk for an H x S x d call under the configuration in force; raise
+    NklError naming the first broken invariant.  Returns (workgroups, units,
+    split blocks, most parts of one block)."""
+    info = (ctypes.c_long * 4)()
+    call("nkl_flash_attn_plan_check", int(H), int(S), int(d), 2 if f16 else 1, info)
+    return tuple(info)
 
 
 def call(name: str, *args) -> int:

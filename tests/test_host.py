@@ -358,3 +358,48 @@ def test_ops_reject_mismatched_operands_before_launching():
         ops.linear_into(a, torch.zeros(5, 7), torch.empty(4, 5))    # weight [N, K] with K != 8
     with pytest.raises(ValueError):
         ops.linear_into(a, torch.zeros(5, 8), torch.empty(4, 5), residual=torch.zeros(4, 4))
+
+
+PLAN_SHAPES = [(1, 1, 128), (1, 64, 128), (1, 128, 128), (1, 4096, 128), (8, 2048, 128), (16, 2048, 128),
+               (3, 1000, 128), (5, 77, 64), (7, 333, 32), (64, 512, 128), (128, 128, 64), (2, 8192, 128),
+               (1, 65, 96), (40, 2049, 128)]
+
+
+@pytest.mark.parametrize("kernel", [None, "teams", "teams4", "w1", "w1o2", "w64", "w64x4", "fwd", "pp", "ks"])
+def test_attention_work_split_covers_every_unit_once(kernel):
+    """The host restatement of the kernels' own walk (each range from its last
+    segment to its first, split blocks merged by their last range, two
+    partial-state slots per range): every (query block, key tile) unit once,
+    for every kernel, schedule, block size and block start cost the
+    configuration accepts, including ragged sizes and more blocks than CUs."""
+    from nkilab import _lib
+
+    try:
+        for sched in (None, "balanced", "pairs", "block"):
+            for qb in (None, 64, 128):
+                for cpb in (None, 0, 1, 7, 40):
+                    _lib.flash_configure(kernel=kernel, schedule=sched, qb=qb, cpb=cpb)
+                    for H, S, d in PLAN_SHAPES:
+                        for f16 in (False, True):
+                            grid, units, split, parts = _lib.flash_plan_check(H, S, d, f16)
+                            assert grid >= 1 and units >= 1 and parts >= 1
+                            if sched != "balanced" and sched is not None:
+                                assert split == 0
+    finally:
+        _lib.flash_configure()
+
+
+def test_attention_work_split_at_the_largest_shapes():
+    """Default plans where 64-bit schedule arithmetic takes over (units past
+    2^31 / costs past 2^32 at 32 heads x 2^20 positions) and where the
+    32-bit instances run (checked against the 64-bit ones on every range)."""
+    from nkilab import _lib
+
+    _lib.flash_configure()
+    for H, S in ((32, 16384), (1, 1 << 18), (256, 4096)):
+        grid, units, split, parts = _lib.flash_plan_check(H, S, 128)
+        assert units > 0 and grid >= 1
+    with pytest.raises(ValueError):
+        _lib.flash_plan_check(1, 128, 128 + 8)
+    with pytest.raises(_lib.NklError):
+        _lib.call("nkl_flash_attn_plan_check", 1, 128, 128, 0, None)  # fp32
