@@ -1301,6 +1301,16 @@ Config choose(int H, int S, int d, bool f16) {
                : units128 < 200 * cus  ? Config{128, kBalanced, kFwdPP}
                : units128 < 1024 * cus ? Config{128, kBalanced, kW32x4x2}
                                        : Config{128, kPairs, kW32x4x2};
+  if (cfg.qb == 64) {
+    // One workgroup per 64-query block when the heaviest block (S / 32 key
+    // tiles) is at most twice a balanced range: a range would then split
+    // blocks into parts as long as a whole block, and pay their merge for
+    // nothing (1 x 128: 14.4 -> 7.9 us, 1 x 256 15.7 -> 9.0, 1 x 512 15.3 ->
+    // 11.6; 1 x 1024 stays balanced, 15.3 against 16.2).
+    const long units64 = (long)H * (2 * (((long)S + 63) / 64 - 1) * (((long)S + 63) / 64) / 2 + (S - 1) / BN + 1);
+    const long range = units64 / cus > kMinUnits ? units64 / cus : kMinUnits;
+    if ((S - 1) / BN + 1 <= 2 * range) cfg.sched = kBlock;
+  }
   const Overrides& ov = overrides();
   if (ov.sched >= 0) cfg.sched = ov.sched;
   if (ov.qb >= 0) cfg.qb = ov.qb;
