@@ -52,8 +52,8 @@ def _no_alloc(q, k, v):
 # split blocks may vary between launches, and the 64-key-tile kernel over
 # balanced ranges, whose merges are in a fixed order (bitwise reproducible).
 CASES = [
-    (None, [(8, 8, 2048, 128), (2, 2, 512, 128)]),
-    (None, [(8, 2, 1024, 64), (4, 1, 300, 64)]),
+    (None, [(8, 8, 2048, 128), (2, 2, 1024, 128)]),
+    (None, [(8, 2, 1024, 64), (4, 1, 600, 64)]),
     (dict(kernel="fwd", schedule="balanced"), [(8, 8, 2048, 128), (3, 3, 700, 128)]),
 ]
 
