@@ -45,7 +45,8 @@ void launch_flash_ks(const AttnArgs& a, const fsched::Work& w, hipStream_t st);
 size_t flash_ks_part_bytes();
 // Process-wide kernel / schedule / block / start-cost overrides (-1: automatic).
 int flash_bf16_configure(int kern, int sched, int qb, int cpb);
-// Process-wide poll budget of the workgroup that merges a split block (-1: 4096).
+// Process-wide poll budget of the workgroup that merges a split block (-1: the
+// planner's choice).
 int flash_bf16_configure_polls(int polls);
 // Host-side check of the launch plan's work split (flash_bf16.hip).
 int flash_bf16_plan_check(int H, int S, int d, bool f16, long* info);

@@ -56,6 +56,10 @@ constexpr int BN = 32;  // keys per tile
 // Smallest unit range a workgroup is given in the balanced schedule (16 left
 // half the CUs idle at 2 x 2048: 24.7 -> 20.6 us at 8; 2 x 1024: 25.5 -> 17.6).
 constexpr long kMinUnits = 8;
+// The merging workgroup's default poll budget, and the part count (the
+// longest block over the mean range) from which it does not wait at all.
+constexpr int kPolls = 256;
+constexpr long kNoWaitParts = 6;
 
 
 template <int D, int WPT, int NT>
@@ -1147,7 +1151,7 @@ enum Kern { kTeams = 0, kW32x4 = 1, kW64x2 = 2, kW64x4 = 3, kTeams4 = 4, kW32x4x
 // workspace sized by one call fits the launch of the next.
 struct Overrides {
   int sched = -1, qb = -1, kern = -1, cpb = -1;
-  int polls = -1;  // the merging workgroup's poll budget (-1: 4096)
+  int polls = -1;  // the merging workgroup's poll budget (-1: the automatic choice in plan())
 };
 Overrides& overrides() {
   static Overrides o = [] {
@@ -1227,7 +1231,6 @@ Work plan(int H, int S, Config cfg) {
   w.units = (long)H * w.units_head;
   w.sched = cfg.sched;
   w.paired = cfg.sched != kBlock;
-  w.polls = overrides().polls < 0 ? 4096 : overrides().polls;
   if (cfg.sched == kBalanced) {
     // As many workgroups as are resident at once, and no range shorter than
     // kMinUnits: a short range spends most of its time filling the pipeline,
@@ -1259,6 +1262,19 @@ Work plan(int H, int S, Config cfg) {
     w.grid = H * w.nqb;
   }
   w.cost = w.units + (long)H * w.nqb * w.cpb;
+  // The merging workgroup's poll budget (fsched::await_parts).  Waiting pays
+  // while a split block has few parts; when the longest block spans six or
+  // more ranges, the holder of its last range storing its state and leaving
+  // the merge to the last part to arrive is faster (one session, us: 1 x 4096
+  // 21.3-21.6 -> 20.0, 2 x 2048 18.3-18.5 -> 17.1, 1 x 2048 19.7-19.8 ->
+  // 17.4; with fewer parts it was slower: 4 x 2048 18.7-18.9 -> 19.3,
+  // 16 x 2048 31.0-31.3 -> 32.6).  256 polls (~0.15 ms) bound the wait when
+  // the other parts cannot run (another kernel holding the CUs); budgets of
+  // 16 to 4096 timed the same.
+  if (overrides().polls >= 0)
+    w.polls = overrides().polls;
+  else
+    w.polls = cfg.sched == kBalanced && (long)w.last_nt * w.grid >= kNoWaitParts * w.units ? 0 : kPolls;
   // 32-bit schedule arithmetic with magic divisors when every value fits in
   // an int: the largest are (cost + 1) grid (fsched::range_of) and r + delta
   // < 2 head_cost <= 2 cost (the pair index), both at most (cost + 1)

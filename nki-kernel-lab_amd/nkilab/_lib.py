@@ -104,7 +104,7 @@ def flash_configure(kernel: str | None = None, schedule: str | None = None, qb: 
 
 def flash_configure_polls(polls: int | None = None) -> None:
     """Set the poll budget of the workgroup that merges a split query block
-    (None: the default 4096; 0: never wait, the last part to arrive merges)."""
+    (None: the automatic choice; 0: never wait, the last part to arrive merges)."""
     call("nkl_flash_attn_configure_polls", -1 if polls is None else int(polls))
 
 
