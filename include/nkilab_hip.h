@@ -281,7 +281,8 @@ int nkl_flash_attn_configure_polls(int polls);
  * state slots; the pairs and block schedules take every block whole, once.
  * Returns NKL_OK, NKL_EDTYPE for other dtypes, or NKL_EINVAL naming the
  * first violated invariant (or a shape outside d <= 128).  info
- * (NULL or 4 longs): workgroups, units, split blocks, most parts of a block.
+ * (NULL or 5 longs): workgroups, units, split blocks, most parts of a block,
+ * and the merging workgroup's poll budget (-1 without the balanced schedule).
  * No counterpart in the reference (its kernels have no work split).
  */
 int nkl_flash_attn_plan_check(int H, int S, int d, int dtype, long* info);

@@ -1523,6 +1523,7 @@ int flash_bf16_plan_check(int H, int S, int d, bool f16, long* info) {
     info[1] = w.units;
     info[2] = split;
     info[3] = max_parts;
+    info[4] = cfg.sched == kBalanced ? w.polls : -1;
   }
   return NKL_OK;
 }

@@ -108,12 +108,13 @@ def flash_configure_polls(polls: int | None = None) -> None:
     call("nkl_flash_attn_configure_polls", -1 if polls is None else int(polls))
 
 
-def flash_plan_check(H: int, S: int, d: int, f16: bool = False) -> tuple[int, int, int, int]:
+def flash_plan_check(H: int, S: int, d: int, f16: bool = False) -> tuple[int, int, int, int, int]:
     """Check on the host the work split the 16-bit attention kernels would
     walk for an H x S x d call under the configuration in force; raise
     NklError naming the first broken invariant.  Returns (workgroups, units,
-    split blocks, most parts of one block)."""
-    info = (ctypes.c_long * 4)()
+    split blocks, most parts of one block, merge poll budget or -1 without
+    the balanced schedule)."""
+    info = (ctypes.c_long * 5)()
     call("nkl_flash_attn_plan_check", int(H), int(S), int(d), 2 if f16 else 1, info)
     return tuple(info)
 

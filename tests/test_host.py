@@ -381,7 +381,7 @@ def test_attention_work_split_covers_every_unit_once(kernel):
                     _lib.flash_configure(kernel=kernel, schedule=sched, qb=qb, cpb=cpb)
                     for H, S, d in PLAN_SHAPES:
                         for f16 in (False, True):
-                            grid, units, split, parts = _lib.flash_plan_check(H, S, d, f16)
+                            grid, units, split, parts, polls = _lib.flash_plan_check(H, S, d, f16)
                             assert grid >= 1 and units >= 1 and parts >= 1
                             if sched != "balanced" and sched is not None:
                                 assert split == 0
@@ -397,9 +397,31 @@ def test_attention_work_split_at_the_largest_shapes():
 
     _lib.flash_configure()
     for H, S in ((32, 16384), (1, 1 << 18), (256, 4096)):
-        grid, units, split, parts = _lib.flash_plan_check(H, S, 128)
+        grid, units, split, parts, polls = _lib.flash_plan_check(H, S, 128)
         assert units > 0 and grid >= 1
     with pytest.raises(ValueError):
         _lib.flash_plan_check(1, 128, 128 + 8)
     with pytest.raises(_lib.NklError):
         _lib.call("nkl_flash_attn_plan_check", 1, 128, 128, 0, None)  # fp32
+
+
+def test_merge_wait_rule():
+    """The workgroup merging a split block waits (a bounded 256 polls) while
+    blocks have few parts, and not at all when the longest block spans six or
+    more ranges; the configured budget overrides both; schedules without split
+    blocks report none."""
+    from nkilab import _lib
+
+    _lib.flash_configure()
+    _lib.flash_configure_polls()
+    try:
+        assert _lib.flash_plan_check(8, 2048, 128)[3:] == (4, 256)   # 4 parts at most: wait
+        assert _lib.flash_plan_check(4, 2048, 128)[4] == 256
+        assert _lib.flash_plan_check(1, 4096, 128)[3:] == (7, 0)    # blocks split 7 ways: no wait
+        assert _lib.flash_plan_check(1, 2048, 128)[4] == 0
+        assert _lib.flash_plan_check(1, 128, 128)[4] == -1          # one workgroup per block
+        assert _lib.flash_plan_check(32, 16384, 128)[4] == -1       # pairs
+        _lib.flash_configure_polls(4096)
+        assert _lib.flash_plan_check(1, 4096, 128)[4] == 4096
+    finally:
+        _lib.flash_configure_polls()
