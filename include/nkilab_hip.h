@@ -199,8 +199,8 @@ int nkl_stream_copy(const void* x, void* y, long nbytes, void* stream);
  * 2^24; *_ss between positions, at most 2^21) and unit stride along d; any
  * S >= 1, 1 <= d <= 128.
  * bf16: P is rounded to bf16 before P.V, statistics and O accumulate in fp32,
- * O is rounded once.  f16: the same with fp16 operands, P and O (the teams
- * or key-split kernel).  f32: everything in fp32.
+ * O is rounded once.  f16: the same with fp16 operands, P and O (the teams,
+ * key-split or one-pass kernel).  f32: everything in fp32.
  */
 int nkl_flash_attn_causal(const void* q, const void* k, const void* v,
                           void* o, int H, int S, int d, long q_sh, long q_ss,
@@ -246,7 +246,10 @@ int nkl_flash_attn_causal_ws(const void* q, const void* k, const void* v,
  *             64-key-tile kernel, 7 the same with its two key-half
  *             wavefronts half an iteration apart, 8 the key-split kernel
  *             (64-query blocks, four wavefronts that each take every
- *             fourth key tile; kernels 6-8 for 64 < d <= 128 only);
+ *             fourth key tile), 9 the one-pass kernel for short sequences
+ *             (S <= 256: one workgroup per 128-query block with every key
+ *             row staged in LDS at once; the default up to S = 224); kernels
+ *             6-9 for 64 < d <= 128 only, others fall back to kernel 0;
  *   schedule: 0 block, 1 balanced (needs the scratch of
  *             nkl_flash_attn_causal_ws), 2 pairs;
  *   qb:       64 or 128 queries per block (kernels 0 and 4);

@@ -43,6 +43,12 @@ size_t flash_fwd_part_bytes();
 // block (the workspace holds two per range).
 void launch_flash_ks(const AttnArgs& a, const fsched::Work& w, hipStream_t st);
 size_t flash_ks_part_bytes();
+// The one-pass kernel for short sequences (flash_tiny.hip): 64 < d <= 128,
+// S <= kTinyMaxS, scale > 0; one workgroup per (head, 128-query block) with
+// every key row of the block staged in LDS at once.  No scratch.
+constexpr int kTinyMaxS = 256;
+bool flash_tiny_fits(const AttnArgs& a);
+void launch_flash_tiny(const AttnArgs& a, hipStream_t st);
 // Process-wide kernel / schedule / block / start-cost overrides (-1: automatic).
 int flash_bf16_configure(int kern, int sched, int qb, int cpb);
 // Process-wide poll budget of the workgroup that merges a split block (-1: the

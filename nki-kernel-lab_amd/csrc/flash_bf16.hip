@@ -60,6 +60,8 @@ constexpr long kMinUnits = 8;
 // longest block over the mean range) from which it does not wait at all.
 constexpr int kPolls = 256;
 constexpr long kNoWaitParts = 6;
+// Longest sequence for which the one-pass kernel (flash_tiny.hip) is chosen.
+constexpr int kTinyAutoS = 224;
 
 
 template <int D, int WPT, int NT>
@@ -1141,12 +1143,23 @@ int cu_count() {
 // (256 registers each, two independent workgroups per CU); or the
 // 64-key-tile kernel of flash_fwd.hip (kFwd: 128-query blocks, two
 // wavefronts per SIMD splitting each tile's keys, LDS-DMA stages).
-enum Kern { kTeams = 0, kW32x4 = 1, kW64x2 = 2, kW64x4 = 3, kTeams4 = 4, kW32x4x2 = 5, kFwd = 6, kFwdPP = 7, kKS = 8 };
+enum Kern {
+  kTeams = 0,
+  kW32x4 = 1,
+  kW64x2 = 2,
+  kW64x4 = 3,
+  kTeams4 = 4,
+  kW32x4x2 = 5,
+  kFwd = 6,
+  kFwdPP = 7,
+  kKS = 8,
+  kTiny = 9
+};
 
 // Launch-configuration overrides (-1: the automatic choice), process-wide:
 // read from the environment once, at first use -- NKL_FLASH_SCHEDULE=
 // block|pairs|balanced, NKL_FLASH_QB=64|128,
-// NKL_FLASH_KERNEL=teams|teams4|w1|w1o2|w64|w64x4|fwd|pp|ks, NKL_FLASH_CPB=<units>
+// NKL_FLASH_KERNEL=teams|teams4|w1|w1o2|w64|w64x4|fwd|pp|ks|tiny, NKL_FLASH_CPB=<units>
 // -- or set by nkl_flash_attn_configure() (tests, tuning), so that a
 // workspace sized by one call fits the launch of the next.
 struct Overrides {
@@ -1175,6 +1188,7 @@ Overrides& overrides() {
       if (!strcmp(f, "fwd")) r.kern = kFwd;
       if (!strcmp(f, "pp")) r.kern = kFwdPP;
       if (!strcmp(f, "ks")) r.kern = kKS;
+      if (!strcmp(f, "tiny")) r.kern = kTiny;
     }
     if (const char* f = getenv("NKL_FLASH_CPB")) r.cpb = min(max(atoi(f), 0), 4096);
     return r;
@@ -1185,7 +1199,7 @@ Overrides& overrides() {
 }  // namespace
 
 int flash_bf16_configure(int kern, int sched, int qb, int cpb) {
-  if (kern < -1 || kern > kKS || sched < -1 || sched > kPairs || (qb != -1 && qb != 64 && qb != 128) || cpb < -1 ||
+  if (kern < -1 || kern > kTiny || sched < -1 || sched > kPairs || (qb != -1 && qb != 64 && qb != 128) || cpb < -1 ||
       cpb > 4096)
     return set_error(NKL_EINVAL, "nkl_flash_attn_configure: kernel %d, schedule %d, qb %d, cpb %d out of range", kern,
                      sched, qb, cpb);
@@ -1327,17 +1341,27 @@ Config choose(int H, int S, int d, bool f16) {
     const long range = units64 / cus > kMinUnits ? units64 / cus : kMinUnits;
     if ((S - 1) / BN + 1 <= 2 * range) cfg.sched = kBlock;
   }
+  // Up to 224 positions (64 < d <= 128), the one-pass kernel: every key row a
+  // 128-query block sees is staged in LDS at once, and nothing is handed over
+  // or merged (same session against one workgroup per 64-query block, us:
+  // 1 x 64 5.0 / 7.3, 1 x 128 6.8 / 7.9, 16 x 128 7.1 / 8.1, 2 x 200 8.6 /
+  // 9.0).  At 256 its longest wavefront walks eight tiles alone and the teams
+  // kernel is faster (1 x 256 9.5 / 9.0, 32 x 256 10.5 / 9.7).
+  if (S <= kTinyAutoS && d > 64 && d <= 128) cfg = Config{128, kBlock, kTiny};
   const Overrides& ov = overrides();
   if (ov.sched >= 0) cfg.sched = ov.sched;
   if (ov.qb >= 0) cfg.qb = ov.qb;
   if (ov.kern >= 0) cfg.kern = ov.kern;
   if (d <= 64 && cfg.kern != kTeams4) cfg.kern = kTeams;
-  if (f16 && cfg.kern != kTeams4 && cfg.kern != kKS) cfg.kern = kTeams;  // fp16: the teams and key-split kernels
+  if (f16 && cfg.kern != kTeams4 && cfg.kern != kKS && cfg.kern != kTiny)
+    cfg.kern = kTeams;  // fp16: the teams, key-split and short-sequence kernels
   if (cfg.kern == kW32x4 || cfg.kern == kW64x2 || cfg.kern == kW32x4x2 || cfg.kern == kFwd || cfg.kern == kFwdPP)
     cfg.qb = 128;
   if (cfg.kern == kW64x4) cfg.qb = 256;
   if (cfg.kern == kKS && (d <= 64 || d > 128)) cfg.kern = kTeams;  // the key-split kernel: 64 < d <= 128
   if (cfg.kern == kKS) cfg.qb = 64;
+  if (cfg.kern == kTiny && (S > kTinyMaxS || d <= 64 || d > 128)) cfg.kern = kTeams;
+  if (cfg.kern == kTiny) cfg = Config{128, kBlock, kTiny};  // one workgroup per 128-query block
   return cfg;
 }
 
@@ -1535,6 +1559,7 @@ int flash_bf16_launch(const AttnArgs& a, void* workspace, size_t workspace_bytes
   // take the teams kernel over the same 64-query blocks (whose partial states
   // have the same size).
   if (cfg.kern == kKS && (a.k_ss != a.v_ss || !(a.c > 0.f))) cfg.kern = kTeams;
+  if (cfg.kern == kTiny && !flash_tiny_fits(a)) cfg.kern = kTeams;  // same blocks and schedule
   if (cfg.sched == kBalanced && !workspace) cfg.sched = kPairs;  // the plain entry point: no scratch
   Work w = plan(a.H, a.S, cfg);
   if (cfg.sched == kBalanced) {
@@ -1547,6 +1572,10 @@ int flash_bf16_launch(const AttnArgs& a, void* workspace, size_t workspace_bytes
     w.part = static_cast<float*>(workspace);
     w.part_bytes = (int)need;
     w.count = counters;
+  }
+  if (cfg.kern == kTiny) {
+    launch_flash_tiny(a, st);
+    return check_launch("nkl_flash_attn_causal");
   }
   if (cfg.kern == kFwd || cfg.kern == kFwdPP) {
     launch_flash_fwd(a, w, cfg.kern == kFwdPP, st);

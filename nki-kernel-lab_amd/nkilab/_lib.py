@@ -90,7 +90,8 @@ def lib() -> ctypes.CDLL:
 
 
 # Codes of nkl_flash_attn_configure (include/nkilab_hip.h).
-FLASH_KERNELS = {"teams": 0, "w1": 1, "w64": 2, "w64x4": 3, "teams4": 4, "w1o2": 5, "fwd": 6, "pp": 7, "ks": 8}
+FLASH_KERNELS = {"teams": 0, "w1": 1, "w64": 2, "w64x4": 3, "teams4": 4, "w1o2": 5, "fwd": 6, "pp": 7, "ks": 8,
+                 "tiny": 9}
 FLASH_SCHEDULES = {"block": 0, "balanced": 1, "pairs": 2}
 
 

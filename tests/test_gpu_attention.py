@@ -220,6 +220,64 @@ def test_flash_bf16_one_wave_per_simd_kernel(rng, flash_cfg, kernel, schedule, H
     np.testing.assert_allclose(out[:, 0], _np(v)[:, 0], rtol=2 ** -8, atol=0)
 
 
+@pytest.mark.parametrize("H,Hkv,S,d", [(1, 1, 1, 128), (1, 1, 128, 128), (1, 1, 256, 128), (3, 3, 77, 128),
+                                       (2, 2, 200, 96), (4, 4, 129, 72), (8, 8, 256, 128), (8, 2, 250, 128),
+                                       (2, 1, 33, 128)])
+@pytest.mark.parametrize("explicit", [False, True])
+def test_flash_short_sequence_kernel(rng, flash_cfg, H, Hkv, S, d, explicit):
+    """The one-pass kernel for S <= 256 (every key row of a 128-query block
+    staged in LDS at once, one workgroup per block), the default up to 224
+    positions for 64 < d <= 128, and forced by name: against fp32 SDPA and the
+    oracle, grouped-query heads included, query 0 seeing only key 0, and
+    repeated calls bitwise equal."""
+    from nkilab import _lib, ops
+
+    if explicit:
+        flash_cfg(kernel="tiny")
+    grid, units, split, parts, polls = _lib.flash_plan_check(H, S, d)
+    assert split == 0 and polls == -1  # one workgroup per block, no scratch
+    q = _bf(rng.standard_normal((H, S, d)))
+    k, v = (_bf(rng.standard_normal((Hkv, S, d))) for _ in range(2))
+    out = ops.attention(q, k, v)
+    kr, vr = (t.repeat_interleave(H // Hkv, dim=0) for t in (k, v))
+    assert_bf16_attention(_np(out), q, kr, vr, (H, Hkv, S, d, explicit))
+    np.testing.assert_allclose(_np(out)[:, 0], _np(vr)[:, 0], rtol=2 ** -8, atol=0)
+    assert torch.equal(ops.attention(q, k, v), out)
+
+
+def test_flash_short_sequence_kernel_largest_row_stride(rng, flash_cfg):
+    """The one-pass kernel's 32-bit copy offsets at the largest row stride the
+    entry points take (2^21 elements) over all 256 rows, in a buffer of NaNs:
+    exact, and the head-dim chunks past d (read from outside the buffer) stay
+    zero rather than NaN."""
+    from nkilab import ops
+
+    flash_cfg(kernel="tiny")
+    H, S, RS, d = 1, 256, 1 << 21, 96
+    buf = torch.full((S, RS), float("nan"), dtype=torch.bfloat16, device="cuda")  # 1 GiB
+    views = []
+    for i in range(3):
+        src = _bf(rng.standard_normal((S, d)))
+        buf[:, 256 * i:256 * i + d] = src
+        views.append(torch.as_strided(buf, (H, S, d), (0, RS, 1), 256 * i))
+    out = _np(ops.attention(*views))
+    assert np.isfinite(out).all()
+    assert_bf16_attention(out, *(t.contiguous() for t in views), ctx=("tiny", d))
+    del buf, views
+
+
+def test_flash_short_sequence_kernel_falls_back_past_its_range(rng, flash_cfg):
+    """Forced where it does not apply (S > 256, d <= 64), the one-pass kernel
+    gives way to the teams kernel: the same results as the default."""
+    from nkilab import ops
+
+    for H, S, d in ((2, 300, 128), (2, 200, 64)):
+        q, k, v = (_bf(rng.standard_normal((H, S, d))) for _ in range(3))
+        flash_cfg(kernel="tiny")
+        out = ops.attention(q, k, v)
+        assert_bf16_attention(_np(out), q, k, v, (H, S, d))
+
+
 @pytest.mark.parametrize("kernel", ["w1", "w1o2", "w64", "w64x4", "teams4", "fwd", "pp", "ks"])
 def test_flash_bf16_one_wave_per_simd_config(flash_cfg, kernel):
     """8 x 2048 x 128 through each one-wavefront-per-SIMD kernel (balanced):

@@ -135,6 +135,23 @@ def test_attention_fp16_key_split_kernel(rng, flash_cfg, schedule, H, Hkv, S, d)
     assert torch.equal(ops.attention(q, k, v), out)
 
 
+@pytest.mark.parametrize("H,Hkv,S,d", [(1, 1, 128, 128), (3, 3, 77, 96), (8, 2, 256, 128), (2, 2, 1, 128)])
+def test_attention_fp16_short_sequence_kernel(rng, flash_cfg, H, Hkv, S, d):
+    """The one-pass kernel for S <= 256 in fp16 (the default up to 224): within
+    1e-3 of fp32 SDPA, grouped-query heads included, and bitwise
+    reproducible."""
+    from nkilab import ops
+
+    flash_cfg(kernel="tiny")
+    q = _h(rng.standard_normal((H, S, d)))
+    k, v = (_h(rng.standard_normal((Hkv, S, d))) for _ in range(2))
+    out = ops.attention(q, k, v)
+    ref = _sdpa_cpu(_np(q), *(np.repeat(_np(t), H // Hkv, axis=0) for t in (k, v)))
+    assert rel_err(_np(out), ref) <= 1e-3, (H, Hkv, S, d)
+    np.testing.assert_allclose(_np(out)[:, 0], _np(v)[:, 0].repeat(H // Hkv, axis=0), rtol=2 ** -11, atol=0)
+    assert torch.equal(ops.attention(q, k, v), out)
+
+
 def test_attention_fp16_gqa_and_kernel_override(rng, flash_cfg):
     """Grouped-query fp16 attention; a kernel override to a bf16-only form
     falls back to the teams kernel for fp16."""

@@ -365,7 +365,7 @@ PLAN_SHAPES = [(1, 1, 128), (1, 64, 128), (1, 128, 128), (1, 4096, 128), (8, 204
                (1, 65, 96), (40, 2049, 128)]
 
 
-@pytest.mark.parametrize("kernel", [None, "teams", "teams4", "w1", "w1o2", "w64", "w64x4", "fwd", "pp", "ks"])
+@pytest.mark.parametrize("kernel", [None, "teams", "teams4", "w1", "w1o2", "w64", "w64x4", "fwd", "pp", "ks", "tiny"])
 def test_attention_work_split_covers_every_unit_once(kernel):
     """The host restatement of the kernels' own walk (each range from its last
     segment to its first, split blocks merged by their last range, two
