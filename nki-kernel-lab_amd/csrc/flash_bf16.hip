@@ -1344,9 +1344,9 @@ Config choose(int H, int S, int d, bool f16) {
   // Up to 224 positions (64 < d <= 128), the one-pass kernel: every key row a
   // 128-query block sees is staged in LDS at once, and nothing is handed over
   // or merged (same session against one workgroup per 64-query block, us:
-  // 1 x 64 5.0 / 7.3, 1 x 128 6.8 / 7.9, 16 x 128 7.1 / 8.1, 2 x 200 8.6 /
-  // 9.0).  At 256 its longest wavefront walks eight tiles alone and the teams
-  // kernel is faster (1 x 256 9.5 / 9.0, 32 x 256 10.5 / 9.7).
+  // 1 x 64 4.6 / 7.4, 1 x 128 6.0 / 7.9, 16 x 128 6.3 / 8.1, 2 x 200 7.4 /
+  // 9.0).  At 256 its longest wavefront walks eight tiles alone and the two
+  // tie (1 x 256 9.0 / 9.0, 32 x 256 9.7 / 9.6).
   if (S <= kTinyAutoS && d > 64 && d <= 128) cfg = Config{128, kBlock, kTiny};
   const Overrides& ov = overrides();
   if (ov.sched >= 0) cfg.sched = ov.sched;

@@ -2,7 +2,8 @@
 // the one-pass kernel for short sequences.
 //
 // One workgroup per (head, 128-query block), the heavier block first; four
-// wavefronts, wavefront w owning queries 128 b + 32 w .. 128 b + 32 w + 31.
+// wavefronts compute, wavefront w owning queries 128 b + 32 w .. + 31, and
+// four more only help issue the copies.
 // Every key row the block can see (at most 256, whole 32-key tiles) is copied
 // global -> LDS at once by the buffer unit (buffer_load ... lds: lane l's 16
 // bytes land at the instruction's LDS base + 16 l), K rows then V rows, 256
@@ -34,7 +35,8 @@ using namespace fsched;
 
 constexpr int TY_BN = 32;                     // keys per tile
 constexpr int TY_QB = 128;                    // queries per block
-constexpr int TY_NW = 4;                      // wavefronts
+constexpr int TY_NW = 4;                      // wavefronts that compute
+constexpr int TY_NC = 8;                      // wavefronts that copy (the last four only copy)
 constexpr int TY_ROWB = 256;                  // bytes of a 128-element 16-bit row
 constexpr int TY_VOFF = kTinyMaxS * TY_ROWB;  // V rows follow the K rows
 constexpr int TY_LDS = 2 * TY_VOFF;           // 128 KB
@@ -50,7 +52,7 @@ __device__ __forceinline__ bf16x8 read_vt16(const unsigned char* a, const unsign
 }  // namespace
 
 template <bool H>
-__global__ __launch_bounds__(64 * TY_NW) void flash_tiny_kernel(AttnArgs p) {
+__global__ __launch_bounds__(64 * TY_NC) void flash_tiny_kernel(AttnArgs p) {
   prefetch_kernargs<sizeof(AttnArgs)>();
   constexpr int D = 128, NQF = D / 16, NDB = D / 32;
   __shared__ __align__(16) unsigned char lds[TY_LDS];
@@ -67,7 +69,8 @@ __global__ __launch_bounds__(64 * TY_NW) void flash_tiny_kernel(AttnArgs p) {
   const int nrow = (nk + TY_BN - 1) / TY_BN * TY_BN;          // rows staged: whole tiles, rows past nk read as 0
 
   // ---- every K and V row of the block into LDS.  Copy n (rows 4 n .. 4 n + 3,
-  // 1 KB) is wavefront n % 4's; lane l fills row 4 n + l / 16, physical chunk
+  // 1 KB) is wavefront n % 8's (a wavefront issues a copy every ~80 ns, so
+  // eight share them); lane l fills row 4 n + l / 16, physical chunk
   // l % 16, which holds logical chunk (l % 16) ^ row_swz(row).  Chunks past d
   // get an offset past the buffer's range and read as zeros.
   {
@@ -82,7 +85,7 @@ __global__ __launch_bounds__(64 * TY_NW) void flash_tiny_kernel(AttnArgs p) {
     const unsigned vbase = kbase + TY_VOFF;
     const int ncopy = nrow / 4;
 #pragma unroll 1
-    for (int n = wq; n < ncopy; n += TY_NW) {
+    for (int n = wq; n < ncopy; n += TY_NC) {
       const int row = 4 * n + (lane >> 4);
       const int lc = (lane & 15) ^ row_swz(row);
       const bool ok = lc * 8 < dlim;
@@ -104,12 +107,12 @@ __global__ __launch_bounds__(64 * TY_NW) void flash_tiny_kernel(AttnArgs p) {
 #pragma unroll
     for (int f = 0; f < NQF; ++f) {
       const int dd = 16 * f + 8 * h32;
-      qf[f] = __builtin_bit_cast(bf16x8, ld16_or_zero(Q, (long)myq * p.q_ss + dd, myq < S && dd < dlim));
+      qf[f] = __builtin_bit_cast(bf16x8, ld16_or_zero(Q, (long)myq * p.q_ss + dd, wq < TY_NW && myq < S && dd < dlim));
     }
   }
   __builtin_amdgcn_s_waitcnt(0);  // this wavefront's copies (and Q) have landed
   __syncthreads();                // ... and every other wavefront's
-  if (qw >= S) return;            // a wavefront wholly past the sequence (uniform)
+  if (wq >= TY_NW || qw >= S) return;  // a copy-only wavefront, or one wholly past the sequence
 
   // Per-lane byte offsets of the MFMA operands within tile 0 (row_swz depends
   // on the row modulo 16, so every tile shares them).
@@ -228,7 +231,7 @@ bool flash_tiny_fits(const AttnArgs& a) {
 
 void launch_flash_tiny(const AttnArgs& a, hipStream_t st) {
   const int nqb = (a.S + TY_QB - 1) / TY_QB;
-  const dim3 grid((unsigned)(a.H * nqb)), block(64 * TY_NW);
+  const dim3 grid((unsigned)(a.H * nqb)), block(64 * TY_NC);
   if (a.f16)
     flash_tiny_kernel<true><<<grid, block, 0, st>>>(a);
   else
