@@ -107,7 +107,8 @@ __global__ __launch_bounds__(64 * TY_NC) void flash_tiny_kernel(AttnArgs p) {
 #pragma unroll
     for (int f = 0; f < NQF; ++f) {
       const int dd = 16 * f + 8 * h32;
-      qf[f] = __builtin_bit_cast(bf16x8, ld16_or_zero(Q, (long)myq * p.q_ss + dd, wq < TY_NW && myq < S && dd < dlim));
+      const bool ok = wq < TY_NW && myq < S && dd < dlim;  // copy-only wavefronts load none
+      qf[f] = __builtin_bit_cast(bf16x8, ld16_or_zero(Q, (long)myq * p.q_ss + dd, ok));
     }
   }
   __builtin_amdgcn_s_waitcnt(0);  // this wavefront's copies (and Q) have landed
