@@ -39,7 +39,14 @@ def _sdpa_cpu(q, k, v):
 # The oracle's flash attention in bf16 arithmetic (the reference's algorithm:
 # 128-query x 128-key tiles, P rounded to bf16 before P V) on the same bf16
 # inputs, kept for the last few input sets (the parametrised tests repeat them).
+# The benchmark configurations are held to 3e-3 of it.  On random shapes the
+# kernels' 32-key tiles and lazily raised max round P to bf16 at other scales
+# than the oracle's 128-key tiles, and the two bf16 outputs differ by up to
+# 3.4e-3 (80 seeded random shapes, H 1-4, S 1-700, d 64/96/128: one above
+# 3e-3, at 1 x 437 x 96; 1 x 225 x 128 gives 3.07e-3), as the oracle itself
+# is up to 3.1e-3 from fp32 SDPA: random shapes are held to 4e-3.
 ORACLE_TOL = 3e-3
+ORACLE_TOL_RANDOM = 4e-3
 _oracle_cache: dict = {}
 
 
@@ -53,14 +60,14 @@ def _oracle_bf16(qn, kn, vn, variant="flash_pipelined"):
 
 
 def assert_bf16_attention(out, q, k, v, ctx=(), variant="flash_pipelined"):
-    """A bf16 attention output against fp32 SDPA (BF16_TOL) and against the
-    oracle's same variant (ORACLE_TOL) on the same bf16 inputs; k and v with as
-    many heads as q."""
+    """A bf16 attention output on random inputs against fp32 SDPA (BF16_TOL)
+    and against the oracle's same variant (ORACLE_TOL_RANDOM) on the same bf16
+    inputs; k and v with as many heads as q."""
     qn, kn, vn = (_np(t) for t in (q, k, v))
     err = rel_err(out, _sdpa_cpu(qn, kn, vn))
     assert err <= BF16_TOL, (ctx, "sdpa", err)
     err = rel_err(out, _oracle_bf16(qn, kn, vn, variant))
-    assert err <= ORACLE_TOL, (ctx, "oracle", err)
+    assert err <= ORACLE_TOL_RANDOM, (ctx, "oracle", err)
 
 
 @pytest.mark.parametrize("variant", VARIANTS)
@@ -222,7 +229,7 @@ def test_flash_bf16_one_wave_per_simd_kernel(rng, flash_cfg, kernel, schedule, H
 
 @pytest.mark.parametrize("H,Hkv,S,d", [(1, 1, 1, 128), (1, 1, 128, 128), (1, 1, 256, 128), (3, 3, 77, 128),
                                        (2, 2, 200, 96), (4, 4, 129, 72), (8, 8, 256, 128), (8, 2, 250, 128),
-                                       (2, 1, 33, 128)])
+                                       (2, 1, 33, 128), (1, 1, 224, 120), (1, 1, 225, 128), (5, 5, 31, 80)])
 @pytest.mark.parametrize("explicit", [False, True])
 def test_flash_short_sequence_kernel(rng, flash_cfg, H, Hkv, S, d, explicit):
     """The one-pass kernel for S <= 256 (every key row of a 128-query block
@@ -436,7 +443,7 @@ def test_gqa_attention_matches_sdpa_on_repeated_kv(rng, variant, H, Hkv, S, d):
     outb = _np(ops.attention(qb, kb, vb, variant=variant))
     refb = _sdpa_cpu(_np(qb), rep(_np(kb)), rep(_np(vb)))
     assert rel_err(outb, refb) <= BF16_TOL, ("bf16", variant)
-    assert rel_err(outb, O.ops_attention(_np(qb), _np(kb), _np(vb), variant, O.BF16)) <= ORACLE_TOL
+    assert rel_err(outb, O.ops_attention(_np(qb), _np(kb), _np(vb), variant, O.BF16)) <= ORACLE_TOL_RANDOM
 
 
 @pytest.mark.parametrize("kernel,qb,schedule", [("teams", "128", "balanced"), ("teams", "64", "balanced"),
