@@ -48,9 +48,10 @@ def _no_alloc(q, k, v):
     return o
 
 
-# (config, shapes of the two calls): the automatic choice, whose fold order of
-# split blocks may vary between launches, and the 64-key-tile kernel over
-# balanced ranges, whose merges are in a fixed order (bitwise reproducible).
+# (config, shapes of the two calls): the automatic choice at two head widths,
+# and the 64-key-tile kernel over balanced ranges.  Every second call is
+# smaller than the first and still splits blocks, so it reads scratch the first
+# call left behind.
 CASES = [
     (None, [(8, 8, 2048, 128), (2, 2, 1024, 128)]),
     (None, [(8, 2, 1024, 64), (4, 1, 600, 64)]),
