@@ -491,14 +491,17 @@ __global__ __launch_bounds__(64 * WGM * WGN * KG) void gemm_dma_kernel(GemmArgs 
   // it, ~35 cycles).  With three or more stages, the copies of K-step s+NS-1
   // (into the stage freed at the end of step s-1) are spread over the four
   // sub-steps of step s, NS-2 steps ahead of use; with two stages, the copies
-  // of K-step s+NS go out with the last sub-step, right after the barrier
-  // that frees their stage, one step ahead of use.
+  // of K-step s+NS go out in two parts, the first H2 with the last sub-step,
+  // right after the barrier that frees their stage, the rest with the first
+  // sub-step of step s+1, and must land by the end of step s+1.
   constexpr bool SPREAD = NS >= 3;
   constexpr int NMMA = TM * TN;
   constexpr int Q = (LPT + 3) / 4;  // copies per sub-step when spread
+  constexpr int H2 = (LPT + 1) / 2;  // two stages: copies issued right after the barrier
   // Copies issued after K-step s+1's last one when step s waits for it: with
   // SPREAD, K-steps s+2 .. s+NS-2 and the first 3 Q copies of K-step s+NS-1
-  // (its last ones go out after the wait); otherwise K-steps s+2 .. s+NS-1.
+  // (its last ones go out after the wait); with two stages, none (the wait
+  // takes every copy in flight).
   constexpr int WAITN = SPREAD ? (NS - 3) * LPT + 3 * Q : (NS - 2) * LPT;
   static_assert(!SPREAD || 3 * Q <= LPT, "the last sub-step's share of the copies is not negative");
   // The MFMAs of one sub-step with copies u0 .. u1-1 of K-step sd between them.
@@ -516,9 +519,15 @@ __global__ __launch_bounds__(64 * WGM * WGN * KG) void gemm_dma_kernel(GemmArgs 
   // Steps of the loop: KG K-steps each (a group's K-steps past K copy zeros).
   const int nk = ((K + G_BK - 1) / G_BK + KG - 1) / KG;
   const unsigned char* const glds = lds + kg * STAGE;  // this group's part of stage 0
+  // K-steps 0 .. NS-2, and with two stages the first H2 copies of K-step
+  // NS-1 (step 0 issues the rest, as every step does for the K-step after it).
 #pragma unroll
-  for (int s = 0; s < (SPREAD ? NS - 1 : NS); ++s) dma(s, s);
-  g_wait_vm<(SPREAD ? NS - 2 : NS - 1) * LPT>();  // K-step 0 has landed
+  for (int s = 0; s < NS - 1; ++s) dma(s, s);
+  if constexpr (!SPREAD) {
+#pragma unroll
+    for (int u = 0; u < H2; ++u) dma1(NS - 1, NS - 1, u);
+  }
+  g_wait_vm<(NS - 2) * LPT + (SPREAD ? 0 : H2)>();  // K-step 0 has landed
   barrier();
   bf16x8 fa[2][TM], fb[2][TN];
   frags(glds, 0, fa[0], fb[0]);
@@ -535,6 +544,8 @@ __global__ __launch_bounds__(64 * WGM * WGN * KG) void gemm_dma_kernel(GemmArgs 
       __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of the MFMAs
       if constexpr (SPREAD)
         mma_copy(fa[ks & 1], fb[ks & 1], s + NS - 1, ks * Q, min((ks + 1) * Q, LPT));
+      else if (ks == 0)
+        mma_copy(fa[0], fb[0], s + NS - 1, H2, LPT);  // the rest of K-step s+1
       else
         mmas(fa[ks & 1], fb[ks & 1]);
       __builtin_amdgcn_sched_barrier(0);
@@ -553,7 +564,7 @@ __global__ __launch_bounds__(64 * WGM * WGN * KG) void gemm_dma_kernel(GemmArgs 
     if constexpr (SPREAD)
       mma_copy(fa[1], fb[1], s + NS - 1, 3 * Q, LPT);
     else
-      mma_copy(fa[1], fb[1], s + NS, 0, LPT);  // into K-step s's stage
+      mma_copy(fa[1], fb[1], s + NS, 0, H2);  // into K-step s's stage
   }
   __builtin_amdgcn_s_waitcnt(0);  // the copies of K-steps past K have landed
 
