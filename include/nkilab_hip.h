@@ -265,10 +265,11 @@ int nkl_flash_attn_configure(int kernel, int schedule, int qb, int cpb);
  * Test and tuning control, process-wide, of the balanced schedule: the poll
  * budget (0 .. 2^20; -1 for the automatic choice: 256, or 0 when the longest
  * block spans six or more ranges) of the workgroup that merges a split query
- * block while it waits for the block's other parts.  Past the
- * budget it stores its own state and arrives like the others, and the last to
- * arrive merges; the parts are folded in the same order either way, so every
- * budget gives the same bits.  No counterpart in the reference (its kernels
+ * block while it waits for the block's other parts (the 128-query teams
+ * kernel folds each part as it arrives).  Past the budget it stores its own
+ * state (or what it has folded so far) and arrives like the others, and the
+ * last to arrive merges the rest; the parts are folded in the same order
+ * either way, so every budget gives the same bits.  No counterpart in the reference (its kernels
  * have no split blocks).
  */
 int nkl_flash_attn_configure_polls(int polls);

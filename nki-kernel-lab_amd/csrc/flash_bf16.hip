@@ -59,6 +59,13 @@ constexpr long kMinUnits = 8;
 // The merging workgroup's default poll budget, and the part count (the
 // longest block over the mean range) from which it does not wait at all.
 constexpr int kPolls = 256;
+// Split blocks of up to kMaskParts parts (teams kernel) record arrivals as a
+// bit per part in the block's counter: part vf + i sets bit i, the holder of
+// the last range kHolderBit, with the number of parts it folded before it
+// gave up waiting from bit kFoldShift.
+constexpr int kMaskParts = 24;
+constexpr int kHolderBit = 1 << 24;
+constexpr int kFoldShift = 25;
 constexpr long kNoWaitParts = 6;
 // Longest sequence for which the one-pass kernel (flash_tiny.hip) is chosen.
 constexpr int kTinyAutoS = 224;
@@ -547,54 +554,162 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), prsrc, poff(vidx, slot, k), 0,
                                                kDeviceCoherent);
       };
-      // The holder of the block's last range waits for the other parts to
-      // arrive instead of storing its own state (see await_parts).
-      const int vl = vf + nparts - 1;
-      if (vidx == vl) await_parts(&w.count[hh * w.nqb + b], nparts, w.polls, arrival);
-      if (vidx != vl || arrival != nparts - 1) {
-        if (keeps) {
-#pragma unroll
-          for (int j = 0; j < OWN; ++j)
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-              pstore(4 * (own0 + j) + k,
-                     make_float4(own[j][4 * k], own[j][4 * k + 1], own[j][4 * k + 2], own[j][4 * k + 3]));
-        }
-        if (team == 0) pstore(L::NCO, make_float4(m_run, l_tot, 0.f, 0.f));
-        // Release: every wavefront's device-coherent stores have completed
-        // (vmcnt) before the barrier and so before the arrival atomic.
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (tid == 0) arrival = atomicAdd(&w.count[hh * w.nqb + b], 1);
-        __syncthreads();
-      }
-      if (arrival == nparts - 1) {  // last to arrive: merge the others and write O
-        // The others' states were complete before their arrivals, which
-        // precede this one; device-coherent loads read them from memory.
-        // The parts are folded last range first, whichever workgroup arrived
-        // last, so the result is bitwise reproducible: the holder of the last
-        // range (the usual last arriver) starts from its own registers; any
-        // other restarts from an empty state and reads its own part back (a
-        // fold into an empty state copies a part exactly).
-        if (vidx != vl) {
-          m_run = -INFINITY;
-          l_tot = 0.f;
-#pragma unroll
-          for (int j = 0; j < OWN; ++j)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) own[j][e] = 0.f;
-        }
-#pragma unroll 1
-        for (int v2 = vl; v2 >= vf; --v2) {
-          if (v2 == vidx && vidx == vl) continue;
+      if constexpr (WPT == 4 && NT == 2) {  // 128-query blocks, two teams
+        // The parts are folded in one order whoever merges: the last range's
+        // state first, then the others from the first range up.  The holder of
+        // the last range walks that segment last, when the block's first part
+        // (walked first by its range) has long been stored, so it folds the
+        // parts from its registers as each arrives (a bit per part in the
+        // block's counter) instead of after the slowest.  Past its poll budget
+        // it stores what it has folded so far, with how many parts that is,
+        // and arrives; the part that completes the counter then merges the
+        // rest.  A fold into an empty state copies a part exactly, so every
+        // path gives the same bits.  Blocks of more than kMaskParts parts count
+        // arrivals instead, and their holder does not wait.
+        const int vl = vf + nparts - 1;
+        int* const cnt = &w.count[hh * w.nqb + b];
+        const bool masked = nparts <= kMaskParts;
+        const int full = ((1 << (nparts - 1)) - 1) | kHolderBit;  // masked: every part in
+        auto load_part = [&](int v2) __attribute__((always_inline)) {
           const int slot2 = range_start_x<F>(v2, w) >= bstart ? 0 : 1;
           fold_state([&](int k) __attribute__((always_inline)) {
             return __builtin_bit_cast(float4,
                                       __builtin_amdgcn_raw_buffer_load_b128(prsrc, poff(v2, slot2, k), 0, kDeviceCoherent));
           });
+        };
+        auto store_state = [&]() __attribute__((always_inline)) {
+          if (keeps) {
+#pragma unroll
+            for (int j = 0; j < OWN; ++j)
+#pragma unroll
+              for (int k = 0; k < 4; ++k)
+                pstore(4 * (own0 + j) + k,
+                       make_float4(own[j][4 * k], own[j][4 * k + 1], own[j][4 * k + 2], own[j][4 * k + 3]));
+          }
+          if (team == 0) pstore(L::NCO, make_float4(m_run, l_tot, 0.f, 0.f));
+          // Release: every wavefront's device-coherent stores have completed
+          // (vmcnt) before the barrier and so before the arrival atomic.
+          __builtin_amdgcn_s_waitcnt(0);
+          __syncthreads();
+        };
+        int from = nparts;  // merging: fold parts vf + from .. vl - 1 after the start state (nparts: not merging)
+        bool start_own = false;  // the start state is this workgroup's registers (else vl's stored state)
+        if (vidx == vl && masked) {
+          // m: the arrivals last read (one poll serves every part already in).
+          int j = 0, budget = w.polls, m = 0;
+          for (; j < nparts - 1; ++j) {
+            if (!((m >> j) & 1)) {
+              if (tid == 0) {
+                int mm = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                while (!((mm >> j) & 1) && budget > 0) {
+                  --budget;
+                  __builtin_amdgcn_s_sleep(8);
+                  mm = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                arrival = mm;
+              }
+              __syncthreads();
+              m = arrival;
+              __syncthreads();
+              if (!((m >> j) & 1)) break;
+            }
+            load_part(vf + j);
+          }
+          if (j == nparts - 1) {
+            from = nparts - 1;  // all folded
+            start_own = true;
+          } else {  // out of budget: hand over what is folded
+            store_state();
+            if (tid == 0) {
+              const int add = kHolderBit | (j << kFoldShift);
+              arrival = ((atomicOr(cnt, add) | add) & full) == full;
+            }
+            __syncthreads();
+            if (arrival) {  // the awaited part came in meanwhile: this workgroup is last
+              from = j;
+              start_own = true;
+            }
+          }
+        } else {
+          store_state();
+          if (tid == 0) {
+            if (masked) {
+              const int bit = vidx == vl ? kHolderBit : 1 << (vidx - vf);
+              const int now = atomicOr(cnt, bit) | bit;
+              arrival = (now & full) == full ? (now >> kFoldShift) & 63 : -1;  // last: parts the holder folded
+            } else {
+              arrival = atomicAdd(cnt, 1) == nparts - 1 ? 0 : -1;
+            }
+          }
+          __syncthreads();
+          if (arrival >= 0) from = arrival;
+          start_own = vidx == vl;
         }
-        store_out();
-        if (tid == 0) atomicExch(&w.count[hh * w.nqb + b], 0);
+        if (from < nparts) {  // this workgroup merges
+          if (!start_own) {
+            m_run = -INFINITY;
+            l_tot = 0.f;
+#pragma unroll
+            for (int j = 0; j < OWN; ++j)
+#pragma unroll
+              for (int e = 0; e < 16; ++e) own[j][e] = 0.f;
+            load_part(vl);
+          }
+#pragma unroll 1
+          for (int j = from; j < nparts - 1; ++j) load_part(vf + j);
+          store_out();
+          if (tid == 0) atomicExch(cnt, 0);
+        }
+      } else {
+        // The holder of the block's last range waits for the other parts to
+        // arrive instead of storing its own state (see await_parts).
+        const int vl = vf + nparts - 1;
+        if (vidx == vl) await_parts(&w.count[hh * w.nqb + b], nparts, w.polls, arrival);
+        if (vidx != vl || arrival != nparts - 1) {
+          if (keeps) {
+#pragma unroll
+            for (int j = 0; j < OWN; ++j)
+#pragma unroll
+              for (int k = 0; k < 4; ++k)
+                pstore(4 * (own0 + j) + k,
+                       make_float4(own[j][4 * k], own[j][4 * k + 1], own[j][4 * k + 2], own[j][4 * k + 3]));
+          }
+          if (team == 0) pstore(L::NCO, make_float4(m_run, l_tot, 0.f, 0.f));
+          // Release: every wavefront's device-coherent stores have completed
+          // (vmcnt) before the barrier and so before the arrival atomic.
+          __builtin_amdgcn_s_waitcnt(0);
+          __syncthreads();
+          if (tid == 0) arrival = atomicAdd(&w.count[hh * w.nqb + b], 1);
+          __syncthreads();
+        }
+        if (arrival == nparts - 1) {  // last to arrive: merge the others and write O
+          // The others' states were complete before their arrivals, which
+          // precede this one; device-coherent loads read them from memory.
+          // The parts are folded last range first, whichever workgroup arrived
+          // last, so the result is bitwise reproducible: the holder of the last
+          // range (the usual last arriver) starts from its own registers; any
+          // other restarts from an empty state and reads its own part back (a
+          // fold into an empty state copies a part exactly).
+          if (vidx != vl) {
+            m_run = -INFINITY;
+            l_tot = 0.f;
+#pragma unroll
+            for (int j = 0; j < OWN; ++j)
+#pragma unroll
+              for (int e = 0; e < 16; ++e) own[j][e] = 0.f;
+          }
+#pragma unroll 1
+          for (int v2 = vl; v2 >= vf; --v2) {
+            if (v2 == vidx && vidx == vl) continue;
+            const int slot2 = range_start_x<F>(v2, w) >= bstart ? 0 : 1;
+            fold_state([&](int k) __attribute__((always_inline)) {
+              return __builtin_bit_cast(float4,
+                                        __builtin_amdgcn_raw_buffer_load_b128(prsrc, poff(v2, slot2, k), 0, kDeviceCoherent));
+            });
+          }
+          store_out();
+          if (tid == 0) atomicExch(&w.count[hh * w.nqb + b], 0);
+        }
       }
     }
     lds_barrier();  // the LDS is restaged by the next segment

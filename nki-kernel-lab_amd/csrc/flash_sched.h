@@ -329,7 +329,9 @@ __device__ __forceinline__ Seg decode_seg_x(long u, long u0, const Work& w) {
 // when blocks are split into many parts); past that `arrival` is -1 and the
 // workgroup stores its state and arrives like the others, the last of which
 // merges.  Either way the states are folded in the
-// same order, so the result does not depend on which workgroup merges.
+// same order, so the result does not depend on which workgroup merges.  (The
+// teams kernel's 128-query form has its own protocol, which folds each part
+// as it arrives; see flash_bf16.hip.)
 __device__ __forceinline__ void await_parts(int* count, int nparts, int polls, int& arrival) {
   if (threadIdx.x == 0) {
     int n = 0;
