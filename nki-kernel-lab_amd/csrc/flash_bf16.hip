@@ -59,11 +59,13 @@ constexpr long kMinUnits = 8;
 // The merging workgroup's default poll budget, and the part count (the
 // longest block over the mean range) from which it does not wait at all.
 constexpr int kPolls = 256;
-// Split blocks of up to kMaskParts parts (teams kernel) record arrivals as a
-// bit per part in the block's counter: part vf + i sets bit i, the holder of
-// the last range kHolderBit, with the number of parts it folded before it
-// gave up waiting from bit kFoldShift.
-constexpr int kMaskParts = 24;
+// Split blocks of up to kMaskParts parts (the teams kernel's 128-query form)
+// record arrivals as a bit per part in the block's counter: part vf + i sets
+// bit i, the holder of the last range kHolderBit, with the number of parts it
+// folded before it gave up waiting from bit kFoldShift.  Blocks of more parts
+// count arrivals and their holder does not wait, which is also where the
+// planner's no-wait rule (kNoWaitParts) applies.
+constexpr int kMaskParts = 6;
 constexpr int kHolderBit = 1 << 24;
 constexpr int kFoldShift = 25;
 constexpr long kNoWaitParts = 6;
@@ -569,7 +571,7 @@ void flash_bf16_kernel(AttnArgs p, Work w) {
         const int vl = vf + nparts - 1;
         int* const cnt = &w.count[hh * w.nqb + b];
         const bool masked = nparts <= kMaskParts;
-        const int full = ((1 << (nparts - 1)) - 1) | kHolderBit;  // masked: every part in
+        const int full = masked ? ((1 << (nparts - 1)) - 1) | kHolderBit : 0;  // masked: every part in
         auto load_part = [&](int v2) __attribute__((always_inline)) {
           const int slot2 = range_start_x<F>(v2, w) >= bstart ? 0 : 1;
           fold_state([&](int k) __attribute__((always_inline)) {

@@ -329,6 +329,34 @@ def test_flash_bf16_balanced_block_start_cost(rng, flash_cfg, kernel, qb, cpb, H
         np.testing.assert_array_equal(_np(ops.attention(q, k, v)), out)
 
 
+# (H, S, most parts of a split block): the 128-query teams form folds blocks of
+# up to six parts as the parts arrive (a bit per part in the block's counter;
+# 3 x 1537 at a poll budget of 0, where the holder folds what is in and hands
+# the rest over) and counts the arrivals of blocks of more parts.
+@pytest.mark.parametrize("H,S,parts", [(8, 2048, 4), (6, 2048, 5), (3, 1537, 6), (2, 4096, 8), (1, 6144, 11)])
+def test_teams_128_merge_protocols(flash_cfg, H, S, parts):
+    """The teams kernel with 128-query blocks over balanced ranges, on shapes
+    that take each merge protocol: within 4e-3 of fp32 SDPA (the bound of the
+    random-shape tests), repeated calls bitwise equal, and a poll budget of 0
+    (every holder gives up at once) gives the same bits."""
+    from nkilab import _lib, ops, workloads
+
+    flash_cfg(kernel="teams", schedule="balanced", qb=128)
+    assert _lib.flash_plan_check(H, S, 128)[3] == parts
+    q, k, v = (t.cuda() for t in workloads.attention_inputs(H, S, 128))
+    want = ops.attention(q, k, v)
+    torch.cuda.synchronize()
+    assert rel_err(_np(want), _sdpa_cpu(*(_np(t) for t in (q, k, v)))) <= 4e-3
+    for _ in range(2):
+        assert torch.equal(ops.attention(q, k, v), want), (H, S)
+    _lib.flash_configure_polls(0)
+    try:
+        for _ in range(2):
+            assert torch.equal(ops.attention(q, k, v), want), (H, S, "polls 0")
+    finally:
+        _lib.flash_configure_polls()
+
+
 @pytest.mark.parametrize("kernel", [None, "teams", "teams4", "w1o2", "w64x4", "fwd", "ks"])
 @pytest.mark.parametrize("H,S,d", [(8, 2048, 128), (3, 1537, 128), (1, 4096, 128), (5, 300, 64)])
 def test_balanced_merge_without_polling_gives_the_same_bits(flash_cfg, kernel, H, S, d):
