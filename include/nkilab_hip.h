@@ -248,7 +248,9 @@ int nkl_flash_attn_causal_ws(const void* q, const void* k, const void* v,
  *             (64-query blocks, four wavefronts that each take every
  *             fourth key tile), 9 the one-pass kernel for short sequences
  *             (S <= 256: one workgroup per 128-query block with every key
- *             row staged in LDS at once; the default up to S = 224); kernels
+ *             row staged in LDS at once; the default up to S = 224, and
+ *             up to 256 for launches of fewer than 12 units of 128 queries
+ *             x 32 keys per CU); kernels
  *             6-9 for 64 < d <= 128 only, others fall back to kernel 0;
  *   schedule: 0 block, 1 balanced (needs the scratch of
  *             nkl_flash_attn_causal_ws), 2 pairs;

@@ -69,7 +69,8 @@ constexpr int kMaskParts = 6;
 constexpr int kHolderBit = 1 << 24;
 constexpr int kFoldShift = 25;
 constexpr long kNoWaitParts = 6;
-// Longest sequence for which the one-pass kernel (flash_tiny.hip) is chosen.
+// Longest sequence for which the one-pass kernel (flash_tiny.hip) is always
+// chosen; up to kTinyMaxS it is chosen for launches in the 64-query regime.
 constexpr int kTinyAutoS = 224;
 
 
@@ -1462,9 +1463,13 @@ Config choose(int H, int S, int d, bool f16) {
   // 128-query block sees is staged in LDS at once, and nothing is handed over
   // or merged (same session against one workgroup per 64-query block, us:
   // 1 x 64 4.6 / 7.4, 1 x 128 6.0 / 7.9, 16 x 128 6.3 / 8.1, 2 x 200 7.4 /
-  // 9.0).  At 256 its longest wavefront walks eight tiles alone and the two
-  // tie (1 x 256 9.0 / 9.0, 32 x 256 9.7 / 9.6).
-  if (S <= kTinyAutoS && d > 64 && d <= 128) cfg = Config{128, kBlock, kTiny};
+  // 9.0; 256 x 224 23.5 against 36.1-37.9).  Up to 256 while the launch is
+  // small enough for 64-query blocks (one session against the default before
+  // this rule, us: 1 x 232 8.1 / 9.0, 1 x 256 8.2 / 9.0, 8 x 256 8.9 / 9.3,
+  // 32 x 256 9.4 / 9.7, 128 x 256 13.5 / 19.8); from there the 128-query
+  // teams kernel is faster (256 x 256 23.0 against 25.1).
+  if (d > 64 && d <= 128 && (S <= kTinyAutoS || (S <= kTinyMaxS && cfg.qb == 64)))
+    cfg = Config{128, kBlock, kTiny};
   const Overrides& ov = overrides();
   if (ov.sched >= 0) cfg.sched = ov.sched;
   if (ov.qb >= 0) cfg.qb = ov.qb;
