@@ -1450,14 +1450,23 @@ Config choose(int H, int S, int d, bool f16) {
                : units128 < 1024 * cus ? Config{128, kBalanced, kW32x4x2}
                                        : Config{128, kPairs, kW32x4x2};
   if (cfg.qb == 64) {
-    // One workgroup per 64-query block when the heaviest block (S / 32 key
-    // tiles) is at most twice a balanced range: a range would then split
-    // blocks into parts as long as a whole block, and pay their merge for
-    // nothing (1 x 128: 14.4 -> 7.9 us, 1 x 256 15.7 -> 9.0, 1 x 512 15.3 ->
-    // 11.6; 1 x 1024 stays balanced, 15.3 against 16.2).
-    const long units64 = (long)H * (2 * (((long)S + 63) / 64 - 1) * (((long)S + 63) / 64) / 2 + (S - 1) / BN + 1);
+    // One workgroup per 64-query block when every block fits one round of
+    // workgroups and the heaviest block (S / 32 key tiles) is at most 3.5
+    // balanced ranges: ranges would then split blocks into parts about as
+    // long as a whole block, and pay their merges for little (1 x 128: 14.4
+    // -> 7.9 us, 1 x 256 15.7 -> 9.0, 1 x 512 15.3 -> 11.6; one session, us:
+    // 1 x 768 15.1 -> 14.0, 10 x 1024 17.7 -> 17.0, 14 x 1024 19.9 -> 17.3;
+    // 8 x 1024, at 4 ranges, stays balanced: 14.7 against 16.8).  With more
+    // blocks than a round holds, 128-query blocks over balanced ranges
+    // (same session, us: 40 x 512 18.2 -> 16.0, 64 x 512 22.1 -> 17.9,
+    // 20 x 1024 20.8 -> 20.7).
+    const long nqb64 = ((long)S + 63) / 64;
+    const long units64 = (long)H * (2 * (nqb64 - 1) * nqb64 / 2 + (S - 1) / BN + 1);
     const long range = units64 / cus > kMinUnits ? units64 / cus : kMinUnits;
-    if ((S - 1) / BN + 1 <= 2 * range) cfg.sched = kBlock;
+    if ((long)H * nqb64 > cus)
+      cfg = Config{128, kBalanced, kTeams};
+    else if (2L * ((S - 1) / BN + 1) <= 7 * range)
+      cfg.sched = kBlock;
   }
   // Up to 224 positions (64 < d <= 128), the one-pass kernel: every key row a
   // 128-query block sees is staged in LDS at once, and nothing is handed over

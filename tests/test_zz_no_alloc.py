@@ -54,7 +54,7 @@ def _no_alloc(q, k, v):
 # call left behind.
 CASES = [
     (None, [(8, 8, 2048, 128), (2, 2, 1024, 128)]),
-    (None, [(8, 2, 1024, 64), (4, 1, 600, 64)]),
+    (None, [(8, 2, 1024, 64), (4, 1, 1000, 64)]),
     (dict(kernel="fwd", schedule="balanced"), [(8, 8, 2048, 128), (3, 3, 700, 128)]),
 ]
 
