@@ -1428,12 +1428,16 @@ Work plan(int H, int S, Config cfg) {
 
 // Schedule and kernel choice, from measured launches on MI355X (units of
 // 128-query blocks per CU): below 12, 64-query blocks halve the unit and keep
-// every CU busy (1 x 4096: 8); up to 48 the 8-wavefront teams kernel over
+// every CU busy (1 x 4096: 8); up to 100 the 8-wavefront teams kernel over
 // balanced ranges (whole blocks leave CUs idle or unevenly loaded; 6 x 2048:
 // 24.5 us against 27.2 for the ping-pong kernel, 12 x 2048 30.8 against
-// 31.6); up to 200 the ping-pong 64-key-tile kernel (flash_fwd.hip) for
-// d > 64, whose steady state is faster (8 x 4096 48.5 against 49.4 us,
-// 4 x 8192 81.0 against 83.9; the teams kernel takes d <= 64 and fp16); from 200
+// 31.6; with its 128-query merge folding parts as they arrive, one session,
+// us: 24 x 2048 44.8 against 47.1, 28 x 2048 51.3 / 54.1, 40 x 2048 67.9 /
+// 70.9, 2 x 8192 47.5 / 49.7, 10 x 4096 61.0 / 61.9, level at 32 x 2048 and
+// 12 x 4096, 8 x 4096 47.1-47.4 / 46.8); up to 200 the ping-pong 64-key-tile
+// kernel (flash_fwd.hip) for d > 64, whose steady state is faster (16 x 4096
+// 83.5 against 85.8-86.1 us, 4 x 8192 78.9 against 81.7, 5 x 8192 102.2
+// against 104.8; the teams kernel takes d <= 64 and fp16); from 200
 // the software-pipelined kernel at two wavefronts per SIMD (d > 64), whose
 // steady state is faster and whose longer segments amortise its start-up;
 // from 1024 one workgroup per pair of blocks, which balances as well and
@@ -1445,7 +1449,7 @@ Config choose(int H, int S, int d, bool f16) {
   const long nqb = (S + 127) / 128;
   const long units128 = (long)H * (2 * (nqb - 1) * nqb + (S - 1) / BN + 1);
   Config cfg = units128 < 12 * cus     ? Config{64, kBalanced, kTeams}
-               : units128 < 48 * cus   ? Config{128, kBalanced, kTeams}
+               : units128 < 100 * cus  ? Config{128, kBalanced, kTeams}
                : units128 < 200 * cus  ? Config{128, kBalanced, kFwdPP}
                : units128 < 1024 * cus ? Config{128, kBalanced, kW32x4x2}
                                        : Config{128, kPairs, kW32x4x2};
