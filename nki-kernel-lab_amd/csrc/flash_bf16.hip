@@ -1455,32 +1455,36 @@ Config choose(int H, int S, int d, bool f16) {
                                        : Config{128, kPairs, kW32x4x2};
   if (cfg.qb == 64) {
     // One workgroup per 64-query block when every block fits one round of
-    // workgroups and the heaviest block (S / 32 key tiles) is at most 3.5
+    // workgroups and the heaviest block (S / 32 key tiles) is at most three
     // balanced ranges: ranges would then split blocks into parts about as
     // long as a whole block, and pay their merges for little (1 x 128: 14.4
-    // -> 7.9 us, 1 x 256 15.7 -> 9.0, 1 x 512 15.3 -> 11.6; one session, us:
-    // 1 x 768 15.1 -> 14.0, 10 x 1024 17.7 -> 17.0, 14 x 1024 19.9 -> 17.3;
-    // 8 x 1024, at 4 ranges, stays balanced: 14.7 against 16.8).  With more
-    // blocks than a round holds, 128-query blocks over balanced ranges
-    // (same session, us: 40 x 512 18.2 -> 16.0, 64 x 512 22.1 -> 17.9,
-    // 20 x 1024 20.8 -> 20.7).
+    // -> 7.9 us, 1 x 256 15.7 -> 9.0, 1 x 512 15.3 -> 11.6; with inputs
+    // rotated through twice the last-level cache, one session, us: 4 x 768
+    // 15.7 -> 15.4, 14 x 1024 20.5 -> 19.2, 12 x 1024 and 1 x 768 level;
+    // 10 x 1024, at 3.2 ranges, stays balanced: 17.9 against 18.8).  With
+    // more blocks than a round holds, 128-query blocks over balanced ranges
+    // (same session, us: 40 x 512 18.3 -> 16.0, 64 x 512 22.2 -> 18.2,
+    // 20 x 1024 level).
     const long nqb64 = ((long)S + 63) / 64;
     const long units64 = (long)H * (2 * (nqb64 - 1) * nqb64 / 2 + (S - 1) / BN + 1);
     const long range = units64 / cus > kMinUnits ? units64 / cus : kMinUnits;
     if ((long)H * nqb64 > cus)
       cfg = Config{128, kBalanced, kTeams};
-    else if (2L * ((S - 1) / BN + 1) <= 7 * range)
+    else if ((S - 1) / BN + 1 <= 3 * range)
       cfg.sched = kBlock;
   }
   // Up to 224 positions (64 < d <= 128), the one-pass kernel: every key row a
   // 128-query block sees is staged in LDS at once, and nothing is handed over
   // or merged (same session against one workgroup per 64-query block, us:
   // 1 x 64 4.6 / 7.4, 1 x 128 6.0 / 7.9, 16 x 128 6.3 / 8.1, 2 x 200 7.4 /
-  // 9.0; 256 x 224 23.5 against 36.1-37.9).  Up to 256 while the launch is
-  // small enough for 64-query blocks (one session against the default before
-  // this rule, us: 1 x 232 8.1 / 9.0, 1 x 256 8.2 / 9.0, 8 x 256 8.9 / 9.3,
-  // 32 x 256 9.4 / 9.7, 128 x 256 13.5 / 19.8); from there the 128-query
-  // teams kernel is faster (256 x 256 23.0 against 25.1).
+  // 9.0; 256 x 224 23.5 against 36.1-37.9; with inputs rotated through twice
+  // the last-level cache, against the teams kernel: 1 x 64 5.1 / 7.2, 1 x 128
+  // 7.1 / 8.2, 16 x 128 7.7 / 8.6, 2 x 200 8.7 / 10.1).  Up to 256 while the
+  // launch is small enough for 64-query blocks (LLC-resident inputs, one
+  // session against the default before this rule, us: 1 x 232 8.1 / 9.0,
+  // 1 x 256 8.2 / 9.0, 8 x 256 8.9 / 9.3, 128 x 256 13.5 / 19.8; rotated
+  // inputs: 1 x 256 9.95 / 10.17, 8 x 256 and 128 x 256 level); from there
+  // the 128-query teams kernel is faster (256 x 256 23.0 against 25.1).
   if (d > 64 && d <= 128 && (S <= kTinyAutoS || (S <= kTinyMaxS && cfg.qb == 64)))
     cfg = Config{128, kBlock, kTiny};
   const Overrides& ov = overrides();
