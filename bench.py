@@ -174,8 +174,8 @@ def bench_attention_sweep(reps, warmup):
     from nkilab import ops, workloads
 
     out = []
-    for H, S in ((1, 256), (1, 1024), (1, 2048), (8, 512), (8, 1024), (2, 2048), (4, 2048), (8, 2048), (16, 2048),
-                 (8, 4096)):
+    for H, S in ((1, 64), (1, 128), (16, 128), (2, 200), (1, 256), (1, 1024), (1, 2048), (8, 512), (8, 1024),
+                 (2, 2048), (4, 2048), (8, 2048), (16, 2048), (8, 4096)):
         q, k, v = (t.cuda() for t in workloads.attention_inputs(H, S, 128))
         sets = n_sets(4 * H * S * 128 * 2)
         bufs = [(q.clone(), k.clone(), v.clone(), torch.empty_like(q)) for _ in range(sets)]
