@@ -405,6 +405,31 @@ def test_attention_work_split_at_the_largest_shapes():
         _lib.call("nkl_flash_attn_plan_check", 1, 128, 128, 0, None)  # fp32
 
 
+def test_kernel_choice_rules():
+    """The automatic kernel and schedule at the boundaries they were measured
+    at (a 256-CU device): the one-pass kernel (one workgroup per 128-query
+    block, no scratch) up to 224 positions and up to 256 in the 64-query
+    regime; 64-query blocks one workgroup each while the heaviest block is
+    within three balanced ranges and every block fits one round; 128-query
+    teams over balanced ranges past one round of 64-query blocks and up to 100
+    units per CU; the 64-key ping-pong kernel beyond.  Units are 32-key tiles
+    of a query block for the teams kernel and 64-key tiles for the ping-pong
+    kernel."""
+    from nkilab import _lib
+
+    _lib.flash_configure()
+    _lib.flash_configure_polls()
+    plan = lambda H, S: _lib.flash_plan_check(H, S, 128)  # noqa: E731
+    assert plan(1, 128)[0] == 1 and plan(1, 128)[2:] == (0, 1, -1)
+    assert plan(8, 256)[0] == 8 * 2 and plan(8, 256)[4] == -1       # one-pass, 128-query blocks
+    assert plan(256, 256)[:2] == (256, 256 * 12)                    # 128-query teams, balanced
+    assert plan(12, 1024)[0] == 12 * 16 and plan(12, 1024)[4] == -1  # 64-query blocks, one each
+    assert plan(10, 1024)[2] > 0                                    # 3.2 ranges: balanced
+    assert plan(64, 512)[1] == 64 * 40 and plan(64, 512)[2] > 0     # 512 64-query blocks: 128-query
+    assert plan(24, 2048)[1] == 24 * 544                            # 51 units per CU: teams
+    assert plan(16, 4096)[1] == 16 * 2112 // 2                      # 132 units per CU: ping-pong
+
+
 def test_merge_wait_rule():
     """The workgroup merging a split block waits (a bounded 256 polls) while
     blocks have few parts, and not at all when the longest block spans six or
