@@ -1485,7 +1485,17 @@ Config choose(int H, int S, int d, bool f16) {
   // 1 x 256 8.2 / 9.0, 8 x 256 8.9 / 9.3, 128 x 256 13.5 / 19.8; rotated
   // inputs: 1 x 256 9.95 / 10.17, 8 x 256 and 128 x 256 level); from there
   // the 128-query teams kernel is faster (256 x 256 23.0 against 25.1).
-  if (d > 64 && d <= 128 && (S <= kTinyAutoS || (S <= kTinyMaxS && cfg.qb == 64)))
+  // Either way while its workgroups (one per head and 128-query block) fit
+  // one round, or the launch is too small for balanced ranges to give every
+  // CU kMinUnits units, or every head is one 64-query tile pair; past that,
+  // 128-query teams over balanced ranges (inputs rotated through twice the
+  // last-level cache, two sessions, us: 512 x 128 20.2 against 22.1-22.2,
+  // 1024 x 128 38.3 against 41.8, 256 x 224 22.9 against 23.9-24.1; the
+  // one-pass kernel stays at 256 x 128, one round: 11.6 against 17.3,
+  // 257 x 128, 129 ranges: 18.1 against 24.2, and 1024 x 64: 23.7 against
+  // 26.7).
+  const bool tiny_fits = (long)H * nqb <= cus || units128 < kMinUnits * cus || S <= 64;
+  if (d > 64 && d <= 128 && (S <= kTinyAutoS || (S <= kTinyMaxS && cfg.qb == 64)) && tiny_fits)
     cfg = Config{128, kBlock, kTiny};
   const Overrides& ov = overrides();
   if (ov.sched >= 0) cfg.sched = ov.sched;

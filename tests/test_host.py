@@ -409,7 +409,8 @@ def test_kernel_choice_rules():
     """The automatic kernel and schedule at the boundaries they were measured
     at (a 256-CU device): the one-pass kernel (one workgroup per 128-query
     block, no scratch) up to 224 positions and up to 256 in the 64-query
-    regime; 64-query blocks one workgroup each while the heaviest block is
+    regime, unless its workgroups need two rounds where balanced ranges fill
+    every CU; 64-query blocks one workgroup each while the heaviest block is
     within three balanced ranges and every block fits one round; 128-query
     teams over balanced ranges past one round of 64-query blocks and up to 100
     units per CU; the 64-key ping-pong kernel beyond.  Units are 32-key tiles
@@ -422,6 +423,8 @@ def test_kernel_choice_rules():
     plan = lambda H, S: _lib.flash_plan_check(H, S, 128)  # noqa: E731
     assert plan(1, 128)[0] == 1 and plan(1, 128)[2:] == (0, 1, -1)
     assert plan(8, 256)[0] == 8 * 2 and plan(8, 256)[4] == -1       # one-pass, 128-query blocks
+    assert plan(257, 128)[0] == 257 and plan(257, 128)[4] == -1     # one-pass: ranges would idle CUs
+    assert plan(512, 128)[:2] == (256, 512 * 4)                     # two rounds: balanced 128-query
     assert plan(256, 256)[:2] == (256, 256 * 12)                    # 128-query teams, balanced
     assert plan(12, 1024)[0] == 12 * 16 and plan(12, 1024)[4] == -1  # 64-query blocks, one each
     assert plan(10, 1024)[2] > 0                                    # 3.2 ranges: balanced
