@@ -1455,22 +1455,22 @@ Config choose(int H, int S, int d, bool f16) {
                                        : Config{128, kPairs, kW32x4x2};
   if (cfg.qb == 64) {
     // One workgroup per 64-query block when every block fits one round of
-    // workgroups and the heaviest block (S / 32 key tiles) is at most three
-    // balanced ranges: ranges would then split blocks into parts about as
-    // long as a whole block, and pay their merges for little (1 x 128: 14.4
-    // -> 7.9 us, 1 x 256 15.7 -> 9.0, 1 x 512 15.3 -> 11.6; with inputs
-    // rotated through twice the last-level cache, one session, us: 4 x 768
-    // 15.7 -> 15.4, 14 x 1024 20.5 -> 19.2, 12 x 1024 and 1 x 768 level;
-    // 10 x 1024, at 3.2 ranges, stays balanced: 17.9 against 18.8).  With
-    // more blocks than a round holds, 128-query blocks over balanced ranges
-    // (same session, us: 40 x 512 18.3 -> 16.0, 64 x 512 22.2 -> 18.2,
-    // 20 x 1024 level).
+    // workgroups and the heaviest block (S / 32 key tiles) exceeds a balanced
+    // range by at most 18 tiles: a block alone then ends before ranges that
+    // pay the partial-state stores and merges of split blocks (about 6 us,
+    // or 18 tiles of the loop, more fixed cost than a whole block).  Inputs
+    // rotated through twice the last-level cache, one session, us (blocks /
+    // balanced ranges): 4 x 768 15.4 / 15.7, 14 x 1024 19.2 / 20.5, 1 x 768
+    // and 12 x 1024 level; 10 x 1024 18.8 / 17.9, 8 x 1536 24.2 / 21.0.
+    // With more blocks than a round holds, 128-query blocks over balanced
+    // ranges (same protocol, us: 40 x 512 18.3 -> 16.0, 64 x 512 22.2 ->
+    // 18.2, 20 x 1024 level).
     const long nqb64 = ((long)S + 63) / 64;
     const long units64 = (long)H * (2 * (nqb64 - 1) * nqb64 / 2 + (S - 1) / BN + 1);
     const long range = units64 / cus > kMinUnits ? units64 / cus : kMinUnits;
     if ((long)H * nqb64 > cus)
       cfg = Config{128, kBalanced, kTeams};
-    else if ((S - 1) / BN + 1 <= 3 * range)
+    else if ((S - 1) / BN + 1 <= range + 18)
       cfg.sched = kBlock;
   }
   // Up to 224 positions (64 < d <= 128), the one-pass kernel: every key row a

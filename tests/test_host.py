@@ -410,8 +410,9 @@ def test_kernel_choice_rules():
     at (a 256-CU device): the one-pass kernel (one workgroup per 128-query
     block, no scratch) up to 224 positions and up to 256 in the 64-query
     regime, unless its workgroups need two rounds where balanced ranges fill
-    every CU; 64-query blocks one workgroup each while the heaviest block is
-    within three balanced ranges and every block fits one round; 128-query
+    every CU; 64-query blocks one workgroup each while the heaviest block
+    exceeds a balanced range by at most 18 tiles and every block fits one
+    round; 128-query
     teams over balanced ranges past one round of 64-query blocks and up to 100
     units per CU; the 64-key ping-pong kernel beyond.  Units are 32-key tiles
     of a query block for the teams kernel and 64-key tiles for the ping-pong
@@ -426,8 +427,9 @@ def test_kernel_choice_rules():
     assert plan(257, 128)[0] == 257 and plan(257, 128)[4] == -1     # one-pass: ranges would idle CUs
     assert plan(512, 128)[:2] == (256, 512 * 4)                     # two rounds: balanced 128-query
     assert plan(256, 256)[:2] == (256, 256 * 12)                    # 128-query teams, balanced
-    assert plan(12, 1024)[0] == 12 * 16 and plan(12, 1024)[4] == -1  # 64-query blocks, one each
-    assert plan(10, 1024)[2] > 0                                    # 3.2 ranges: balanced
+    assert plan(14, 1024)[0] == 14 * 16 and plan(14, 1024)[4] == -1  # 64-query blocks, one each
+    assert plan(10, 1024)[2] > 0                                    # 32 tiles, ranges of 10: balanced
+    assert plan(8, 1536)[2] > 0                                     # 48 tiles, ranges of 18: balanced
     assert plan(64, 512)[1] == 64 * 40 and plan(64, 512)[2] > 0     # 512 64-query blocks: 128-query
     assert plan(24, 2048)[1] == 24 * 544                            # 51 units per CU: teams
     assert plan(16, 4096)[1] == 16 * 2112 // 2                      # 132 units per CU: ping-pong
